@@ -1,0 +1,279 @@
+"""Benchmark of the ELSA two-pass attention hot path on one MI355X.
+
+One step = the training-path attention of BASELINE config 2 at the north-star shape:
+two-pass forward with row state (Phase 1 fold on MFMA -> HBM summaries -> Phase 2
+merge) plus the exact-recompute backward (preprocess, dq, dk/dv), B=1 H=8 N=16384
+d=64 fp16, non-causal, synthetic N(0,1) q/k/v/dO (seed 2026) resident in HBM.
+
+Prints ONE JSON line.  ``value`` is the algorithmic fwd+bwd throughput
+(3.5 * 4*B*H*N^2*d flop per step, recompute not counted).  ``kernels`` holds each
+kernel's HIP-event average on the launch stream; ``roofline`` is computed for the
+kernel with the largest share of the step.  ``cpu_baseline`` times the numpy
+restatement of the reference algorithm (oracle/) on a bounded row sample.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "ELSA attn fwd/bwd TFLOP/s + %MFMA peak (B1 H8 d64 16K fp16); ViT-T img/s"
+PEAK_TFLOPS = {"fp16": 2516.6, "bf16": 2516.6, "fp32": 157.3}
+HBM_GBPS = 8000.0
+
+
+def _args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--heads", type=int, default=8)
+    ap.add_argument("--seq", type=int, default=16384)
+    ap.add_argument("--dim", type=int, default=64)
+    ap.add_argument("--dtype", choices=["fp16", "bf16", "fp32"], default="fp16")
+    ap.add_argument("--causal", action="store_true")
+    ap.add_argument("--block-n", type=int, default=None, help="K-partition width (default: planner)")
+    ap.add_argument("--cpu-baseline", dest="cpu_baseline", action="store_true", default=True)
+    ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
+    ap.add_argument("--cpu-rows", type=int, default=512, help="query rows of the CPU-baseline sample")
+    ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "traffic_north_star.json"))
+    return ap.parse_args()
+
+
+def _flops_fwd(b, h, n, d, causal):
+    return 4.0 * b * h * d * (n * (n + 1) / 2 if causal else n * n)
+
+
+def main() -> int:
+    args = _args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures a single GPU: this build has no multi-GPU path (the attention shards by "
+              "heads with no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr, flush=True)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import elsa_amd
+    from elsa_amd import _lib
+    from elsa_amd.attention import forward_plan
+    from elsa_amd.attention_bwd import _attach_workspace, _bwd_args
+    from elsa_amd.attention import _BiasMeta, _make_fwd_args
+
+    dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[args.dtype]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, N, D = args.batch, args.heads, args.seq, args.dim
+    shape = (B, H, N, D)
+    g = torch.Generator().manual_seed(2026)
+    q, k, v, do = (torch.randn(shape, generator=g).to(dt).to(dev) for _ in range(4))
+    causal = bool(args.causal)
+    print(f"bench: {shape} {args.dtype} causal={causal} steps={args.steps} warmup={args.warmup}", file=sys.stderr,
+          flush=True)
+
+    def step():
+        out, rm, rz = elsa_amd.twopass_attention_with_state(q, k, v, is_causal=causal, block_n=args.block_n)
+        return elsa_amd.twopass_attention_backward(q, k, v, out, do, is_causal=causal, row_m=rm, row_z=rz)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    print(f"bench: step {ms_step:.3f} ms (wall {wall * 1e3 / args.steps:.3f} ms)", file=sys.stderr, flush=True)
+
+    # ---- per-kernel HIP-event timing through the C ABI, on the stream the kernels run on
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    plan = forward_plan(q, is_causal=causal, block_n=args.block_n)
+    out = torch.empty_like(q)
+    rm = torch.empty((B * H, N), device=dev, dtype=torch.float32)
+    rz = torch.empty_like(rm)
+    fa = _make_fwd_args(q, k, v, out, rm, rz, _BiasMeta(None, 0, 0, 0, 0, False), is_causal=causal,
+                        summary_dtype=dt, partition_len=args.block_n, q_chunk=None, scale=1.0 / math.sqrt(D))
+    ws_f = torch.empty(plan["workspace_bytes"], dtype=torch.uint8, device=dev)
+    fa.workspace, fa.workspace_bytes = ws_f.data_ptr(), plan["workspace_bytes"]
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ba = _bwd_args(q, k, v, out, do, rm, rz, dq, dk, dv, _BiasMeta(None, 0, 0, 0, 0, False), is_causal=causal,
+                   scale=1.0 / math.sqrt(D))
+    ws_b = _attach_workspace(lib, ba, dev)
+    qc = plan["q_chunk"]
+    chunks = [(s, min(qc, N - s)) for s in range(0, N, qc)]
+
+    launches = {
+        "phase1_fold": lambda: [lib.elsa_phase1(ctypes.byref(fa), s, n, sh) for s, n in chunks],
+        "phase2_merge": lambda: [lib.elsa_phase2(ctypes.byref(fa), s, n, sh) for s, n in chunks],
+        "bwd_preprocess": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 0, sh)],
+        "bwd_dq": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 1, sh)],
+        "bwd_dkdv": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 2, sh)],
+    }
+    kern_ms = {}
+    for name, fn in launches.items():
+        for rc in fn():
+            _lib.check(rc, name)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        kern_ms[name] = e0.elapsed_time(e1) / args.steps
+    print("bench: kernels " + ", ".join(f"{k_}={v_:.3f}ms" for k_, v_ in kern_ms.items()), file=sys.stderr,
+          flush=True)
+
+    # ---- sampled parity check of this very run (closed form, fp64 on CPU)
+    rows = np.random.default_rng(0).choice(N, 16, replace=False)
+    qs = q[:, :, rows].float().cpu().double().numpy()
+    kk = k.float().cpu().double().numpy()
+    vv = v.float().cpu().double().numpy()
+    sc = np.einsum("bhid,bhjd->bhij", qs, kk) / math.sqrt(D)
+    if causal:
+        sc = np.where(np.arange(N)[None, None, None, :] <= rows[None, None, :, None], sc, -np.inf)
+    sc -= sc.max(-1, keepdims=True)
+    p = np.exp(sc)
+    p /= p.sum(-1, keepdims=True)
+    ref_o = np.einsum("bhij,bhjd->bhid", p, vv)
+    max_abs = float(np.abs(out[:, :, rows].float().cpu().double().numpy() - ref_o).max())
+
+    # ---- derived numbers
+    f_fwd = _flops_fwd(B, H, N, D, causal)
+    f_bwd = 2.5 * f_fwd
+    peak = PEAK_TFLOPS[args.dtype]
+    ssz = torch.empty((), dtype=dt).element_size()
+    p2_bytes = plan["partitions"] * B * H * N * (8 + D * ssz) + B * H * N * D * ssz + 8 * B * H * N
+    fwd_ms = kern_ms["phase1_fold"] + kern_ms["phase2_merge"]
+    bwd_ms = kern_ms["bwd_preprocess"] + kern_ms["bwd_dq"] + kern_ms["bwd_dkdv"]
+    algo = {  # algorithmic work per launch set (flop, or bytes for the HBM-bound kernels)
+        "phase1_fold": ("mfma", f_fwd),
+        "phase2_merge": ("hbm", p2_bytes),
+        "bwd_preprocess": ("hbm", 2 * B * H * N * D * ssz + 16 * B * H * N),
+        "bwd_dq": ("mfma", 0.5 * f_fwd),
+        "bwd_dkdv": ("mfma", 2.0 * f_fwd),
+    }
+    kernels = {}
+    for name, ms in kern_ms.items():
+        bound, work = algo[name]
+        if bound == "mfma":
+            ach = work / (ms * 1e-3) / 1e12
+            kernels[name] = {"ms": round(ms, 4), "tflops": round(ach, 1), "frac_peak": round(ach / peak, 4)}
+        else:
+            ach = work / (ms * 1e-3) / 1e9
+            kernels[name] = {"ms": round(ms, 4), "gbps": round(ach, 1), "frac_peak": round(ach / HBM_GBPS, 4)}
+    dom = max(kern_ms, key=kern_ms.get)
+    bound, work = algo[dom]
+    traffic = None
+    if os.path.exists(args.traffic_file):
+        try:
+            with open(args.traffic_file) as fh:
+                traffic = json.load(fh).get(dom, {}).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    if bound == "mfma":
+        achieved = work / (kern_ms[dom] * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
+                    "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": dom,
+                    "work_per_launch": work}
+    else:
+        achieved = work / (kern_ms[dom] * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_GBPS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_GBPS, 4), "traffic": traffic, "kernel": dom,
+                    "work_per_launch": work}
+
+    value = (f_fwd + f_bwd) / (ms_step * 1e-3) / 1e12
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic: q,k,v,dO ~ N(0,1), torch.Generator seed 2026, resident in HBM",
+        "config": {"workload": "ELSA two-pass attention fwd(with row state)+bwd, "
+                               + ("causal" if causal else "non-causal"),
+                   "batch": B, "heads": H, "seq_len": N, "head_dim": D,
+                   "partitions": plan["partitions"], "partition_len": plan["partition_len"],
+                   "q_chunk": plan["q_chunk"]},
+        "fwd_ms": round(fwd_ms, 4),
+        "bwd_ms": round(bwd_ms, 4),
+        "fwd_tflops": round(f_fwd / (fwd_ms * 1e-3) / 1e12, 1),
+        "bwd_tflops": round(f_bwd / (bwd_ms * 1e-3) / 1e12, 1),
+        "fwd_frac_peak": round(f_fwd / (fwd_ms * 1e-3) / 1e12 / peak, 4),
+        "bwd_frac_peak": round(f_bwd / (bwd_ms * 1e-3) / 1e12 / peak, 4),
+        "phase2_gbps": kernels["phase2_merge"]["gbps"],
+        "max_abs_sampled_fwd": max_abs,
+        "kernels": kernels,
+        "roofline": roofline,
+    }
+    if args.cpu_baseline:
+        result["cpu_baseline"] = _cpu_baseline(args, B, H, N, D, causal)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def _cpu_baseline(args, B, H, N, D, causal):
+    """Time the numpy restatement (oracle/) of the reference algorithm on a row sample."""
+    import numpy as np
+
+    from oracle import elsa_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # noqa: BLE001
+        threads = os.cpu_count() or 1
+    rows = np.arange(min(args.cpu_rows, N))
+    q, k, v, do = O.make_inputs((B, H, N, D), seed=2026, dtype=args.dtype, with_dout=True)
+    qs, dos = q[:, :, rows], do[:, :, rows]
+    print(f"bench: cpu baseline on {len(rows)} of {N} query rows, {threads} threads", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    out, rm, rz = O.forward(q, k, v, is_causal=causal, part_len=max(64, N // 2), dtype=args.dtype, mode="ref",
+                            rows=rows)
+    O.backward(qs, k, v, out, dos, rm, rz, is_causal=causal, dtype=args.dtype, mode="ref", rows=rows)
+    secs = time.perf_counter() - t0
+    frac = len(rows) / N
+    flops = 3.5 * _flops_fwd(B, H, N, D, causal) * (frac if not causal else
+                                                   (rows + 1).sum() / (N * (N + 1) / 2))
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(flops / secs / 1e12, 5), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+            "sample": f"numpy restatement (oracle/elsa_oracle.py, reference rounding points) of fwd+bwd for "
+                      f"{len(rows)} of {N} query rows x all {N} keys, B{B} H{H} d{D} {args.dtype}; {secs:.2f} s on "
+                      f"{cpu}, os.cpu_count()={os.cpu_count()}",
+            "seconds": round(secs, 3)}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,283 @@
+"""Training API: forward with row state, recompute backward, autograd and dbias.
+
+Mirrors the reference's attention_bwd.py (``twopass_attention_with_state``
+:77-185, ``twopass_attention_backward`` :661-839, ``_TwopassAttentionAutograd``
+:842-905, ``_dense_bias_backward`` :908-1000, ``twopass_attention_train``
+:1003-1030).  All device work goes to libelsa_hip.so: ``elsa_fwd`` (with row
+state), ``elsa_row_stats`` when the caller has no state, ``elsa_bwd`` (D/LSE2
+preprocess, dq kernel, dk/dv kernel) and ``elsa_dbias``.
+
+Backward tile knobs (``block_m``, ``block_n``, ``num_warps``, ``num_stages``)
+are validated like the reference and otherwise ignored.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Literal, Optional
+
+import torch
+
+from . import _lib
+from .attention import (
+    _canonical_bias,
+    _check_qkv,
+    _elsa_forward,
+    _pad_head_dim,
+    _resolve_forward_options,
+    _resolve_precision,
+    _validate_warps,
+)
+
+
+def twopass_attention_with_state(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    bias: Optional[torch.Tensor] = None,
+    is_causal: bool = False,
+    block_m: Optional[int] = None,
+    block_n: Optional[int] = None,
+    q_chunk_size: Optional[int] = None,
+    summary_dtype: Optional[torch.dtype] = None,
+    phase1_warps: Optional[int] = None,
+    phase2_warps: Optional[int] = None,
+    phase1_stages: Optional[int] = None,
+    phase2_stages: Optional[int] = None,
+    input_precision: Literal["auto", "ieee", "tf32", "tf32x3"] = "auto",
+    algorithm: Literal["auto", "paper_scan"] = "auto",
+    return_contiguous_inputs: bool = False,
+) -> tuple[torch.Tensor, ...]:
+    """Training forward: ``(out, row_m, row_z[, q_c, k_c, v_c])`` with base-2 row state."""
+    _check_qkv(q, k, v, "twopass_attention_with_state")
+    batch, heads, seq_len, head_dim = map(int, q.shape)
+    if seq_len <= 0:
+        empty_state = torch.empty((batch * heads, 0), device=q.device, dtype=torch.float32)
+        out_empty = torch.empty_like(q)
+        if return_contiguous_inputs:
+            return out_empty, empty_state, empty_state, q.contiguous(), k.contiguous(), v.contiguous()
+        return out_empty, empty_state, empty_state
+    if head_dim > 128:
+        raise ValueError("head_dim > 128 is not supported by the current Triton kernels")
+    if algorithm not in ("auto", "paper_scan"):
+        raise ValueError("only algorithm='paper_scan' is available in this strict release")
+    part, qc, sdt = _resolve_forward_options(
+        q, block_m=block_m, block_n=block_n, q_chunk_size=q_chunk_size, summary_dtype=summary_dtype,
+        phase1_warps=phase1_warps, phase2_warps=phase2_warps, phase1_stages=phase1_stages,
+        phase2_stages=phase2_stages, input_precision=input_precision,
+    )
+    out, row_m, row_z, q_c, k_c, v_c = _elsa_forward(
+        q, k, v, bias=bias, is_causal=is_causal, summary_dtype=sdt, partition_len=part, q_chunk=qc, want_state=True
+    )
+    if return_contiguous_inputs:
+        return out, row_m, row_z, q_c, k_c, v_c
+    return out, row_m, row_z
+
+
+def _bwd_args(q_c, k_c, v_c, out_c, do_c, row_m, row_z, dq, dk, dv, bias_meta, *, is_causal, scale):
+    batch, heads, seq_len, head_dim = map(int, q_c.shape)
+    a = _lib.BwdArgs()
+    a.q, a.k, a.v = q_c.data_ptr(), k_c.data_ptr(), v_c.data_ptr()
+    a.out, a.dout = _lib.ptr(out_c), _lib.ptr(do_c)
+    a.row_m, a.row_z = _lib.ptr(row_m), _lib.ptr(row_z)
+    a.dq, a.dk, a.dv = _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv)
+    a.bias = _lib.bias_desc(bias_meta.tensor, (bias_meta.stride_b, bias_meta.stride_h, bias_meta.stride_q,
+                                               bias_meta.stride_k))
+    a.batch, a.heads, a.seq_len, a.head_dim = batch, heads, seq_len, head_dim
+    a.dtype = _lib.dtype_code(q_c.dtype)
+    a.is_causal = 1 if is_causal else 0
+    a.scale = float(scale)
+    return a
+
+
+def _attach_workspace(lib, args, device):
+    nbytes = int(lib.elsa_bwd_workspace_bytes(ctypes.byref(args)))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    args.workspace = ws.data_ptr()
+    args.workspace_bytes = nbytes
+    return ws
+
+
+def _row_stats(q_c, k_c, bias_meta, *, is_causal, scale):
+    lib = _lib.load()
+    bh, n = q_c.shape[0] * q_c.shape[1], q_c.shape[2]
+    row_m = torch.empty((bh, n), dtype=torch.float32, device=q_c.device)
+    row_z = torch.empty_like(row_m)
+    args = _bwd_args(q_c, k_c, k_c, None, None, None, None, None, None, None, bias_meta, is_causal=is_causal,
+                     scale=scale)
+    with torch.cuda.device(q_c.device):
+        _lib.check(lib.elsa_row_stats(ctypes.byref(args), row_m.data_ptr(), row_z.data_ptr(),
+                                      _lib.stream_handle(q_c.device)), "elsa_row_stats")
+    return row_m, row_z
+
+
+def twopass_attention_backward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    out: torch.Tensor,
+    grad_out: torch.Tensor,
+    *,
+    bias: Optional[torch.Tensor] = None,
+    is_causal: bool = False,
+    block_m: Optional[int] = None,
+    block_n: Optional[int] = None,
+    num_warps: Optional[int] = None,
+    num_stages: Optional[int] = None,
+    input_precision: Literal["auto", "ieee", "tf32", "tf32x3"] = "auto",
+    row_m: Optional[torch.Tensor] = None,
+    row_z: Optional[torch.Tensor] = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Recompute backward: ``(dq, dk, dv)`` (reference attention_bwd.py:661-839). No dbias."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must have shape [B,H,N,D]")
+    if q.shape != k.shape or q.shape != v.shape or q.shape != out.shape or q.shape != grad_out.shape:
+        raise ValueError("q, k, v, out, and grad_out must have identical shapes")
+    if q.device.type != "cuda":
+        raise ValueError("twopass_attention_backward currently requires CUDA tensors")
+    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError("supported dtypes are fp16, bf16, and fp32")
+    batch, heads, seq_len, head_dim = map(int, q.shape)
+    if head_dim > 128:
+        raise ValueError("head_dim > 128 is not supported by the current Triton kernels")
+    if seq_len <= 0:
+        return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    _resolve_precision(input_precision, q.dtype)
+    if block_m is not None:
+        max(16, int(block_m))
+    if block_n is not None:
+        max(16, int(block_n))
+    if num_warps is not None:
+        _validate_warps("num_warps", num_warps)
+    for t in (k, v, out, grad_out):
+        if t.dtype != q.dtype:
+            raise ValueError("q, k, v, out, and grad_out must share one dtype")
+    bh = batch * heads
+    scale = 1.0 / math.sqrt(head_dim)
+    lib = _lib.load()
+    q_c, k_c, v_c = (_pad_head_dim(t.contiguous()) for t in (q, k, v))
+    out_c, do_c = (_pad_head_dim(t.contiguous()) for t in (out, grad_out))
+    bias_meta = _canonical_bias(bias, batch=batch, heads=heads, seq_len=seq_len, device=q.device)
+    if row_m is None or row_z is None:
+        row_m, row_z = _row_stats(q_c, k_c, bias_meta, is_causal=is_causal, scale=scale)
+    else:
+        if row_m.shape != (bh, seq_len) or row_z.shape != (bh, seq_len):
+            raise ValueError("row_m and row_z must have shape [B*H,N]")
+        row_m = row_m.contiguous().float()
+        row_z = row_z.contiguous().float()
+    dq = torch.empty_like(q_c)
+    dk = torch.empty_like(k_c)
+    dv = torch.empty_like(v_c)
+    args = _bwd_args(q_c, k_c, v_c, out_c, do_c, row_m, row_z, dq, dk, dv, bias_meta, is_causal=is_causal,
+                     scale=scale)
+    ws = _attach_workspace(lib, args, q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.elsa_bwd(ctypes.byref(args), _lib.stream_handle(q.device)), "elsa_bwd")
+    del ws
+    if q_c.shape[-1] != head_dim:
+        dq, dk, dv = (t[..., :head_dim].contiguous() for t in (dq, dk, dv))
+    return dq, dk, dv
+
+
+def _dense_bias_backward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    out: torch.Tensor,
+    grad_out: torch.Tensor,
+    *,
+    bias: torch.Tensor,
+    is_causal: bool,
+    row_m: Optional[torch.Tensor] = None,
+    row_z: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """dbias summed over the bias's broadcast dims (reference attention_bwd.py:908-1000).
+
+    One HIP kernel covers every bias rank ([N,N], [1|H,N,N], [1|B,1|H,N,N]): it
+    accumulates ``p*(dp - D)`` over the broadcast (b, h) pairs of each output tile
+    without materialising the [B,H,N,N] score tensor, so the reference's 64M-element
+    dense fallback limit does not apply.
+    """
+    batch, heads, seq_len, head_dim = map(int, q.shape)
+    lib = _lib.load()
+    meta = _canonical_bias(bias, batch=batch, heads=heads, seq_len=seq_len, device=q.device)
+    bias_b = 1 if meta.stride_b == 0 else batch
+    bias_h = 1 if meta.stride_h == 0 else heads
+    scale = 1.0 / math.sqrt(head_dim)
+    q_c, k_c, v_c = (_pad_head_dim(t.contiguous()) for t in (q, k, v))
+    out_c, do_c = (_pad_head_dim(t.contiguous()) for t in (out, grad_out))
+    if row_m is None or row_z is None:
+        row_m, row_z = _row_stats(q_c, k_c, meta, is_causal=is_causal, scale=scale)
+    dbias = torch.empty((bias_b, bias_h, seq_len, seq_len), dtype=torch.float32, device=q.device)
+    args = _bwd_args(q_c, k_c, v_c, out_c, do_c, row_m.contiguous(), row_z.contiguous(), None, None, None, meta,
+                     is_causal=is_causal, scale=scale)
+    ws = _attach_workspace(lib, args, q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.elsa_dbias(ctypes.byref(args), dbias.data_ptr(), bias_b, bias_h,
+                                  _lib.stream_handle(q.device)), "elsa_dbias")
+    del ws
+    return dbias.reshape(bias.shape).to(dtype=bias.dtype)
+
+
+class _TwopassAttentionAutograd(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, bias, is_causal, fwd_kwargs, bwd_kwargs):
+        out, row_m, row_z, q_saved, k_saved, v_saved = twopass_attention_with_state(
+            q, k, v, bias=bias, is_causal=is_causal, return_contiguous_inputs=True, **fwd_kwargs
+        )
+        if bias is None:
+            saved_bias = torch.empty(1, device=q.device, dtype=torch.float32)
+            has_bias = False
+        else:
+            saved_bias = bias
+            has_bias = True
+        ctx.save_for_backward(q_saved, k_saved, v_saved, out, saved_bias, row_m, row_z)
+        ctx.has_bias = has_bias
+        ctx.bias_requires_grad = bool(bias is not None and bias.requires_grad)
+        ctx.is_causal = bool(is_causal)
+        ctx.bwd_kwargs = dict(bwd_kwargs)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        q, k, v, out, saved_bias, row_m, row_z = ctx.saved_tensors
+        bias = saved_bias if ctx.has_bias else None
+        dq, dk, dv = twopass_attention_backward(
+            q, k, v, out, grad_out, bias=bias, is_causal=ctx.is_causal, row_m=row_m, row_z=row_z, **ctx.bwd_kwargs
+        )
+        dbias = None
+        if ctx.bias_requires_grad:
+            dbias = _dense_bias_backward(q, k, v, out, grad_out, bias=bias, is_causal=ctx.is_causal, row_m=row_m,
+                                         row_z=row_z)
+        return dq, dk, dv, dbias, None, None, None
+
+
+def twopass_attention_train(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    bias: Optional[torch.Tensor] = None,
+    is_causal: bool = False,
+    bwd_block_m: Optional[int] = None,
+    bwd_block_n: Optional[int] = None,
+    bwd_num_warps: Optional[int] = None,
+    bwd_num_stages: Optional[int] = None,
+    bwd_input_precision: Literal["auto", "ieee", "tf32", "tf32x3"] = "auto",
+    **fwd_kwargs,
+) -> torch.Tensor:
+    """Autograd wrapper: two-pass forward with state plus recompute backward (attention_bwd.py:1003-1030)."""
+    if bwd_input_precision == "auto":
+        fwd_input_precision = fwd_kwargs.get("input_precision")
+        if fwd_input_precision in ("ieee", "tf32", "tf32x3"):
+            bwd_input_precision = fwd_input_precision
+    bwd_kwargs = {
+        "block_m": bwd_block_m,
+        "block_n": bwd_block_n,
+        "num_warps": bwd_num_warps,
+        "num_stages": bwd_num_stages,
+        "input_precision": bwd_input_precision,
+    }
+    bwd_kwargs = {key: value for key, value in bwd_kwargs.items() if value is not None}
+    return _TwopassAttentionAutograd.apply(q, k, v, bias, is_causal, dict(fwd_kwargs), bwd_kwargs)

@@ -1,0 +1,343 @@
+// C ABI of libelsa_hip.so: argument validation, partition routing, workspace
+// layout and the q-chunk loop.  No device memory is allocated here.
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "elsa_hip.h"
+#include "elsa_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  return fail(ELSA_ERR_LAUNCH, "%s: %s", where, hipGetErrorString(e));
+}
+
+size_t dtype_size(int dt) { return dt == ELSA_F32 ? 4 : 2; }
+bool dtype_ok(int dt) { return dt == ELSA_F16 || dt == ELSA_BF16 || dt == ELSA_F32; }
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+double softmax_scale(float s, int d) { return s > 0.f ? (double)s : 1.0 / std::sqrt((double)d); }
+
+int check_common(int batch, int heads, int n, int d, int dtype, const void* q, const void* k, const void* v) {
+  if (batch <= 0 || heads <= 0 || n <= 0 || d <= 0)
+    return fail(ELSA_ERR_INVALID, "batch, heads, seq_len and head_dim must be positive (got %d,%d,%d,%d)", batch,
+                heads, n, d);
+  if (d > 128) return fail(ELSA_ERR_INVALID, "head_dim > 128 is not supported (got %d)", d);
+  if (d % 8 != 0) return fail(ELSA_ERR_INVALID, "head_dim must be a multiple of 8 (got %d)", d);
+  if (!dtype_ok(dtype)) return fail(ELSA_ERR_INVALID, "unknown dtype %d", dtype);
+  if (!q || !k || !v) return fail(ELSA_ERR_INVALID, "q, k and v must be non-null device pointers");
+  if ((int64_t)batch * heads > 65535)
+    return fail(ELSA_ERR_UNSUPPORTED, "batch*heads > 65535 is not supported (got %lld)", (long long)batch * heads);
+  return ELSA_OK;
+}
+
+int check_bias(const elsa_bias_desc& b) {
+  if (b.ptr == nullptr) return ELSA_OK;
+  if (!dtype_ok(b.dtype)) return fail(ELSA_ERR_INVALID, "unknown bias dtype %d", b.dtype);
+  return ELSA_OK;
+}
+
+elsa::BiasView bias_view(const elsa_bias_desc& b) {
+  return elsa::BiasView{b.ptr, b.dtype, b.stride_b, b.stride_h, b.stride_q, b.stride_k};
+}
+
+// Partition routing for 256 CUs: at least ~2048 Phase-1 workgroups when the
+// query side alone does not provide them, partitions of >= 512 keys, and at
+// least two partitions from 8K keys on so long sequences keep the two-pass merge.
+int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
+  if (!a || !pl) return fail(ELSA_ERR_INVALID, "null argument");
+  int rc = check_common(a->batch, a->heads, a->seq_len, a->head_dim, a->dtype, a->q, a->k, a->v);
+  if (rc) return rc;
+  if (!dtype_ok(a->summary_dtype)) return fail(ELSA_ERR_INVALID, "unknown summary_dtype %d", a->summary_dtype);
+  if ((rc = check_bias(a->bias))) return rc;
+  if ((a->row_m == nullptr) != (a->row_z == nullptr))
+    return fail(ELSA_ERR_INVALID, "row_m and row_z must be given together");
+  if (a->partition_len < 0 || a->q_chunk < 0) return fail(ELSA_ERR_INVALID, "partition_len and q_chunk must be >= 0");
+
+  const int64_t n = a->seq_len, bh = (int64_t)a->batch * a->heads, d = a->head_dim;
+  const int dp = elsa::pad_head_dim(a->head_dim);
+  const int waves = n <= 64 ? 2 : 4;
+  const int bm = elsa::kRowsPerWave * waves;
+  const int kt = elsa::phase1_key_tile(a->dtype, dp);
+  const size_t row_bytes = 8 + (size_t)d * dtype_size(a->summary_dtype);
+
+  int64_t part;
+  if (a->partition_len > 0) {
+    part = std::min<int64_t>(a->partition_len, n);
+  } else {
+    const int64_t q_rows = a->q_chunk > 0 ? std::min<int64_t>(a->q_chunk, n) : n;
+    const int64_t q_tiles = bh * cdiv(q_rows, bm);
+    int64_t p = cdiv(2048, q_tiles);
+    p = std::min<int64_t>(p, std::max<int64_t>(1, n / 512));
+    if (n >= 8192) p = std::max<int64_t>(p, 2);
+    p = std::max<int64_t>(p, 1);
+    part = cdiv(cdiv(n, p), kt) * kt;
+    part = std::min<int64_t>(part, n);
+  }
+  const int64_t parts = cdiv(n, part);
+  if (parts > 65535) return fail(ELSA_ERR_UNSUPPORTED, "too many K partitions (%lld)", (long long)parts);
+
+  int64_t q_chunk = a->q_chunk > 0 ? std::min<int64_t>(a->q_chunk, n) : n;
+  if (a->q_chunk == 0) {
+    // keep the summary workspace under 4 GiB by chunking the query rows
+    const size_t cap = size_t(4) << 30;
+    const size_t per_row = (size_t)parts * bh * row_bytes;
+    if (per_row * q_chunk > cap) q_chunk = std::max<int64_t>(bm, (int64_t)(cap / per_row) / bm * bm);
+  }
+  const size_t rows = (size_t)parts * bh * q_chunk;
+  pl->partitions = (int32_t)parts;
+  pl->partition_len = (int32_t)part;
+  pl->q_chunk = (int32_t)q_chunk;
+  pl->block_m = bm;
+  pl->key_tile = kt;
+  pl->_pad = 0;
+  pl->workspace_bytes = 2 * align256(rows * 4) + align256(rows * d * dtype_size(a->summary_dtype));
+  return ELSA_OK;
+}
+
+struct FwdBuffers {
+  float* m;
+  float* z;
+  void* s;
+};
+
+FwdBuffers carve(const elsa_fwd_args* a, const elsa_fwd_plan& pl) {
+  const size_t rows = (size_t)pl.partitions * a->batch * a->heads * pl.q_chunk;
+  char* base = static_cast<char*>(a->workspace);
+  FwdBuffers b;
+  b.m = reinterpret_cast<float*>(base);
+  b.z = reinterpret_cast<float*>(base + align256(rows * 4));
+  b.s = base + 2 * align256(rows * 4);
+  return b;
+}
+
+int run_phase(const elsa_fwd_args* a, const elsa_fwd_plan& pl, int q_start, int q_len, hipStream_t st, int which) {
+  FwdBuffers wb = carve(a, pl);
+  const int bh = a->batch * a->heads;
+  if (which == 1) {
+    elsa::Phase1Params p{};
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.bias = bias_view(a->bias);
+    p.m_buf = wb.m;
+    p.z_buf = wb.z;
+    p.s_buf = wb.s;
+    p.s_dtype = a->summary_dtype;
+    p.H = a->heads;
+    p.N = a->seq_len;
+    p.D = a->head_dim;
+    p.BH = bh;
+    p.q_start = q_start;
+    p.q_len = q_len;
+    p.part_len = pl.partition_len;
+    p.P = pl.partitions;
+    p.causal = a->is_causal ? 1 : 0;
+    p.scale_log2 = (float)(1.4426950408889634 * softmax_scale(a->scale, a->head_dim));
+    p.bias_log2 = 1.4426950408889634f;
+    p.rows_pad = pl.q_chunk;
+    hipError_t e = elsa::launch_phase1(p, a->dtype, pl.block_m / elsa::kRowsPerWave, st);
+    if (e != hipSuccess) return hip_fail(e, "phase1 launch");
+  } else {
+    elsa::Phase2Params p{};
+    p.m_buf = wb.m;
+    p.z_buf = wb.z;
+    p.s_buf = wb.s;
+    p.s_dtype = a->summary_dtype;
+    p.out = a->out;
+    p.out_dtype = a->dtype;
+    p.row_m = a->row_m;
+    p.row_z = a->row_z;
+    p.N = a->seq_len;
+    p.D = a->head_dim;
+    p.BH = bh;
+    p.q_start = q_start;
+    p.q_len = q_len;
+    p.part_len = pl.partition_len;
+    p.P = pl.partitions;
+    p.causal = a->is_causal ? 1 : 0;
+    p.rows_pad = pl.q_chunk;
+    hipError_t e = elsa::launch_phase2(p, st);
+    if (e != hipSuccess) return hip_fail(e, "phase2 launch");
+  }
+  return ELSA_OK;
+}
+
+int check_fwd_call(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
+  int rc = plan_fwd(a, pl);
+  if (rc) return rc;
+  if (!a->out) return fail(ELSA_ERR_INVALID, "out must be a non-null device pointer");
+  if (!a->workspace || a->workspace_bytes < pl->workspace_bytes)
+    return fail(ELSA_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", a->workspace_bytes,
+                pl->workspace_bytes);
+  return ELSA_OK;
+}
+
+int check_rows(const elsa_fwd_args* a, const elsa_fwd_plan& pl, int q_start, int q_len) {
+  if (q_start < 0 || q_len <= 0 || q_start + (int64_t)q_len > a->seq_len || q_len > pl.q_chunk)
+    return fail(ELSA_ERR_INVALID, "row range [%d, %d) invalid for seq_len %d and q_chunk %d", q_start, q_start + q_len,
+                a->seq_len, pl.q_chunk);
+  return ELSA_OK;
+}
+
+int check_bwd(const elsa_bwd_args* a, bool need_grads) {
+  if (!a) return fail(ELSA_ERR_INVALID, "null argument");
+  int rc = check_common(a->batch, a->heads, a->seq_len, a->head_dim, a->dtype, a->q, a->k, a->v);
+  if (rc) return rc;
+  if ((rc = check_bias(a->bias))) return rc;
+  if (need_grads) {
+    if (!a->out || !a->dout || !a->dq || !a->dk || !a->dv)
+      return fail(ELSA_ERR_INVALID, "out, dout, dq, dk and dv must be non-null device pointers");
+    if (!a->row_m || !a->row_z) return fail(ELSA_ERR_INVALID, "row_m and row_z are required");
+  }
+  return ELSA_OK;
+}
+
+elsa::BwdParams bwd_params(const elsa_bwd_args* a) {
+  elsa::BwdParams p{};
+  p.q = a->q;
+  p.k = a->k;
+  p.v = a->v;
+  p.out = a->out;
+  p.dout = a->dout;
+  p.row_m = a->row_m;
+  p.row_z = a->row_z;
+  p.dq = a->dq;
+  p.dk = a->dk;
+  p.dv = a->dv;
+  p.bias = bias_view(a->bias);
+  p.H = a->heads;
+  p.N = a->seq_len;
+  p.D = a->head_dim;
+  p.BH = a->batch * a->heads;
+  p.causal = a->is_causal ? 1 : 0;
+  p.scale = (float)softmax_scale(a->scale, a->head_dim);
+  p.scale_log2 = (float)(1.4426950408889634 * softmax_scale(a->scale, a->head_dim));
+  const size_t rows = (size_t)p.BH * p.N;
+  char* base = static_cast<char*>(a->workspace);
+  p.d_row = reinterpret_cast<float*>(base);
+  p.lse_row = reinterpret_cast<float*>(base + align256(rows * 4));
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int elsa_abi_version(void) { return ELSA_ABI_VERSION; }
+
+const char* elsa_last_error(void) { return g_last_error.c_str(); }
+
+size_t elsa_struct_size(int which) {
+  switch (which) {
+    case 0: return sizeof(elsa_fwd_args);
+    case 1: return sizeof(elsa_fwd_plan);
+    case 2: return sizeof(elsa_bwd_args);
+    case 3: return sizeof(elsa_bias_desc);
+    default: return 0;
+  }
+}
+
+int elsa_fwd_plan_get(const elsa_fwd_args* args, elsa_fwd_plan* plan) { return plan_fwd(args, plan); }
+
+int elsa_fwd(const elsa_fwd_args* a, void* stream) {
+  elsa_fwd_plan pl;
+  int rc = check_fwd_call(a, &pl);
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  for (int q0 = 0; q0 < a->seq_len; q0 += pl.q_chunk) {
+    const int len = std::min(pl.q_chunk, a->seq_len - q0);
+    if ((rc = run_phase(a, pl, q0, len, st, 1))) return rc;
+    if ((rc = run_phase(a, pl, q0, len, st, 2))) return rc;
+  }
+  return ELSA_OK;
+}
+
+int elsa_phase1(const elsa_fwd_args* a, int32_t q_start, int32_t q_len, void* stream) {
+  elsa_fwd_plan pl;
+  int rc = check_fwd_call(a, &pl);
+  if (rc) return rc;
+  if ((rc = check_rows(a, pl, q_start, q_len))) return rc;
+  return run_phase(a, pl, q_start, q_len, static_cast<hipStream_t>(stream), 1);
+}
+
+int elsa_phase2(const elsa_fwd_args* a, int32_t q_start, int32_t q_len, void* stream) {
+  elsa_fwd_plan pl;
+  int rc = check_fwd_call(a, &pl);
+  if (rc) return rc;
+  if ((rc = check_rows(a, pl, q_start, q_len))) return rc;
+  return run_phase(a, pl, q_start, q_len, static_cast<hipStream_t>(stream), 2);
+}
+
+size_t elsa_bwd_workspace_bytes(const elsa_bwd_args* a) {
+  if (!a || a->batch <= 0 || a->heads <= 0 || a->seq_len <= 0) return 0;
+  const size_t rows = (size_t)a->batch * a->heads * a->seq_len;
+  return 2 * align256(rows * 4);
+}
+
+int elsa_bwd(const elsa_bwd_args* a, void* stream) { return elsa_bwd_stage(a, -1, stream); }
+
+int elsa_bwd_stage(const elsa_bwd_args* a, int32_t stage, void* stream) {
+  int rc = check_bwd(a, true);
+  if (rc) return rc;
+  if (stage < -1 || stage > 2) return fail(ELSA_ERR_INVALID, "stage must be -1, 0, 1 or 2 (got %d)", stage);
+  const size_t need = elsa_bwd_workspace_bytes(a);
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(ELSA_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", a->workspace_bytes,
+                need);
+  hipError_t e = elsa::launch_bwd(bwd_params(a), a->dtype, stage, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "backward launch");
+  return ELSA_OK;
+}
+
+int elsa_row_stats(const elsa_bwd_args* a, float* row_m, float* row_z, void* stream) {
+  int rc = check_bwd(a, false);
+  if (rc) return rc;
+  if (!row_m || !row_z) return fail(ELSA_ERR_INVALID, "row_m and row_z must be non-null");
+  hipError_t e = elsa::launch_row_stats(bwd_params(a), row_m, row_z, a->dtype, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "row_stats launch");
+  return ELSA_OK;
+}
+
+int elsa_dbias(const elsa_bwd_args* a, float* dbias, int32_t bias_batch, int32_t bias_heads, void* stream) {
+  int rc = check_bwd(a, false);
+  if (rc) return rc;
+  if (!a->out || !a->dout || !a->row_m || !a->row_z || !dbias)
+    return fail(ELSA_ERR_INVALID, "out, dout, row_m, row_z and dbias must be non-null");
+  if (!(bias_batch == 1 || bias_batch == a->batch) || !(bias_heads == 1 || bias_heads == a->heads))
+    return fail(ELSA_ERR_INVALID, "dbias shape [%d,%d] does not broadcast against [%d,%d]", bias_batch, bias_heads,
+                a->batch, a->heads);
+  const size_t need = elsa_bwd_workspace_bytes(a);
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(ELSA_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", a->workspace_bytes,
+                need);
+  hipError_t e = elsa::launch_dbias(bwd_params(a), dbias, bias_batch, bias_heads, a->dtype,
+                                    static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "dbias launch");
+  return ELSA_OK;
+}
+
+int elsa_debug_mfma(int32_t variant, const void* a, const void* b, float* d, void* stream) {
+  if (variant < 0 || variant > 2) return fail(ELSA_ERR_INVALID, "variant must be 0, 1 or 2");
+  if (!a || !b || !d) return fail(ELSA_ERR_INVALID, "null pointer");
+  hipError_t e = elsa::launch_debug_mfma(variant, a, b, d, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "debug_mfma launch");
+  return ELSA_OK;
+}
+
+}  // extern "C"

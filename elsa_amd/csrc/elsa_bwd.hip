@@ -1,0 +1,516 @@
+// ELSA backward on gfx950: exact recompute of p from the saved base-2 row state.
+//
+//   preprocess  D = rowsum(O * dO), LSE2 = m + log2(max(z, 1e-30))   (attention_bwd.py:188-224)
+//   dq kernel   per 32-row wave tile, loop over 32-key tiles:         (attention_bwd.py:309-412)
+//               S^T = K Q^T, dP^T = V dO^T, p = exp2(S^T*c - LSE2), dS^T = p (dP^T - D)
+//               (cast to the input dtype, :404), dQ^T += K^T dS^T, dq = scale * dQ.
+//   dk/dv kernel per 32-key wave tile, loop over 32-row tiles:        (attention_bwd.py:415-527)
+//               S = Q K^T, dP = dO V^T, p = exp2(S*c - LSE2); dV^T += dO^T p (p cast, :512),
+//               dK^T += Q^T dS (dS cast, :514), dk = scale * dK.
+//   row stats   online (m, z) over all keys when no state was saved   (attention_bwd.py:227-306)
+//   dbias       per 32x32 score tile: sum over broadcast (b, h) of p (dp - D)  (attention_bwd.py:529-624)
+//
+// The same swap23 row permutation as the forward makes the D-layout registers of
+// S^T / S directly usable as the B operand of the following MFMA.
+#include "elsa_internal.h"
+#include "elsa_mfma.h"
+
+namespace elsa {
+
+template <typename T, int DP>
+struct BwdCfg {
+  static constexpr int KP = Mfma<T>::KP;
+  static constexpr int KSTEP = 2 * KP;
+  static constexpr int NKK = DP / KSTEP;
+  static constexpr bool HALF = sizeof(T) == 2;
+  static constexpr int TT = 32;  // keys (dq) or rows (dk/dv) per LDS stage
+  static constexpr int KPAD = HALF ? 8 : 1;
+  static constexpr int VPAD = HALF ? 8 : 1;
+  static constexpr int RS = DP + KPAD;  // row-major tile stride [TT][RS]
+  static constexpr int TS = TT + VPAD;  // transposed tile stride [DP][TS]
+  static constexpr int NDT = DP / 32;
+  static constexpr int NJ = 16 / KP;
+  static constexpr int CE = 16 / (int)sizeof(T);
+};
+
+__device__ inline float load_bias_b(const BiasView& b, int bi, int hi, int row, int key) {
+  const int64_t off = (int64_t)bi * b.sb + (int64_t)hi * b.sh + (int64_t)row * b.sq + (int64_t)key * b.sk;
+  if (b.dtype == ELSA_F32) return static_cast<const float*>(b.ptr)[off];
+  if (b.dtype == ELSA_F16) return static_cast<float>(static_cast<const f16*>(b.ptr)[off]);
+  return static_cast<float>(static_cast<const bf16*>(b.ptr)[off]);
+}
+
+// Copy rows [row0, row0+TT) x [0, DP) of a [N, D] matrix into LDS, row-major
+// (stride RS) and/or transposed (stride TS); rows >= row_end and d >= D are zero.
+template <typename T, int DP, int NT, bool RM, bool TR>
+__device__ inline void stage_tile(const T* __restrict__ src, int row0, int row_end, int D, T* rm, T* tr, int tid) {
+  using C = BwdCfg<T, DP>;
+  constexpr int CPR = DP / C::CE;
+  constexpr int TOTAL = C::TT * CPR;
+#pragma unroll
+  for (int ci = tid; ci < TOTAL; ci += NT) {
+    const int r = ci / CPR, d0 = (ci % CPR) * C::CE;
+    const int ra = row0 + r;
+    Chunk16 v{};
+    if (ra < row_end && d0 < D) v = *reinterpret_cast<const Chunk16*>(src + (int64_t)ra * D + d0);
+    const T* e = reinterpret_cast<const T*>(&v);
+    if constexpr (RM) {
+      if constexpr (C::HALF) {
+        *reinterpret_cast<Chunk16*>(rm + r * C::RS + d0) = v;
+      } else {
+#pragma unroll
+        for (int t = 0; t < C::CE; ++t) rm[r * C::RS + d0 + t] = e[t];
+      }
+    }
+    if constexpr (TR) {
+#pragma unroll
+      for (int t = 0; t < C::CE; ++t) tr[(d0 + t) * C::TS + r] = e[t];
+    }
+  }
+}
+
+// A-operand fragment for rows swap23(c) of a 32-row tile: from the row-major
+// copy for 16-bit types, from the transposed copy for fp32 (one element per lane).
+template <typename T, int DP>
+__device__ inline typename Mfma<T>::frag a_frag(const T* rm, const T* tr, int c, int g, int kk) {
+  using C = BwdCfg<T, DP>;
+  if constexpr (C::HALF) {
+    return *reinterpret_cast<const typename Mfma<T>::frag*>(rm + swap23(c) * C::RS + kk * C::KSTEP + g * C::KP);
+  } else {
+    return tr[(kk * C::KSTEP + g * C::KP) * C::TS + swap23(c)];
+  }
+}
+
+// ------------------------------------------------------------------ preprocess
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdParams p) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)p.BH * p.N) return;
+  const T* o = static_cast<const T*>(p.out) + i * p.D;
+  const T* g = static_cast<const T*>(p.dout) + i * p.D;
+  float acc = 0.f;
+  for (int d = 0; d < p.D; d += 16 / (int)sizeof(T)) {
+    const Chunk16 a = *reinterpret_cast<const Chunk16*>(o + d);
+    const Chunk16 b = *reinterpret_cast<const Chunk16*>(g + d);
+    const T* ea = reinterpret_cast<const T*>(&a);
+    const T* eb = reinterpret_cast<const T*>(&b);
+#pragma unroll
+    for (int t = 0; t < 16 / (int)sizeof(T); ++t) acc = fmaf(static_cast<float>(ea[t]), static_cast<float>(eb[t]), acc);
+  }
+  p.d_row[i] = acc;
+  p.lse_row[i] = p.row_m[i] + __log2f(fmaxf(p.row_z[i], 1.0e-30f));
+}
+
+// ------------------------------------------------------------------ dq
+template <typename T, int DP, int WAVES, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
+  using C = BwdCfg<T, DP>;
+  using M = Mfma<T>;
+  typedef typename M::frag F;
+  constexpr int NT = 64 * WAVES, BM = 32 * WAVES;
+  __shared__ __attribute__((aligned(16))) T Ks[C::HALF ? C::TT * C::RS : 1];
+  __shared__ __attribute__((aligned(16))) T Vs[C::HALF ? C::TT * C::RS : 1];
+  __shared__ __attribute__((aligned(16))) T Kt[DP * C::TS];
+  __shared__ __attribute__((aligned(16))) T Vt[C::HALF ? 1 : DP * C::TS];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int bh = blockIdx.y;
+  const int wg_row0 = blockIdx.x * BM;
+  const int wg_last = min(p.N, wg_row0 + BM) - 1;
+  const int my_row = wg_row0 + wave * 32 + c;
+  const bool row_ok = my_row < p.N;
+  const int64_t hoff = (int64_t)bh * p.N * p.D;
+  const T* Q = static_cast<const T*>(p.q) + hoff;
+  const T* K = static_cast<const T*>(p.k) + hoff;
+  const T* V = static_cast<const T*>(p.v) + hoff;
+  const T* dO = static_cast<const T*>(p.dout) + hoff;
+  const int bi = bh / p.H, hi = bh % p.H;
+
+  F qf[C::NKK], gf[C::NKK];
+  const int rsafe = row_ok ? my_row : 0;
+#pragma unroll
+  for (int kk = 0; kk < C::NKK; ++kk) {
+    const int d0 = kk * C::KSTEP + g * C::KP;
+    qf[kk] = load_frag<T>(Q + (int64_t)rsafe * p.D + d0, row_ok && d0 < p.D);
+    gf[kk] = load_frag<T>(dO + (int64_t)rsafe * p.D + d0, row_ok && d0 < p.D);
+  }
+  const float lse = row_ok ? p.lse_row[(int64_t)bh * p.N + my_row] : 0.f;
+  const float dd = row_ok ? p.d_row[(int64_t)bh * p.N + my_row] : 0.f;
+  const bool live = row_ok && lse > kNegInf;
+
+  f32x16 acc[C::NDT];
+#pragma unroll
+  for (int dt = 0; dt < C::NDT; ++dt) acc[dt] = f32x16{};
+  const int k_end = p.causal ? wg_last + 1 : p.N;
+
+  for (int t0 = 0; t0 < k_end; t0 += C::TT) {
+    __syncthreads();
+    stage_tile<T, DP, NT, C::HALF, true>(K, t0, k_end, p.D, Ks, Kt, tid);
+    stage_tile<T, DP, NT, C::HALF, !C::HALF>(V, t0, k_end, p.D, Vs, Vt, tid);
+    __syncthreads();
+    f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < C::NKK; ++kk) {
+      s = M::mma(a_frag<T, DP>(Ks, Kt, c, g, kk), qf[kk], s);
+      dp = M::mma(a_frag<T, DP>(Vs, Vt, c, g, kk), gf[kk], dp);
+    }
+    const bool full = !HAS_BIAS && (t0 + C::TT <= k_end) && (!p.causal || t0 + C::TT - 1 <= wg_row0 + wave * 32);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = t0 + key_of_reg(r, g);
+      bool ok = live;
+      if (!full) ok = ok && key < k_end && (!p.causal || key <= my_row);
+      float x = s[r] * p.scale_log2;
+      if constexpr (HAS_BIAS) x = ok ? fmaf(load_bias_b(p.bias, bi, hi, my_row, key), kLog2e, x) : x;
+      const float pr = ok ? fast_exp2(x - lse) : 0.f;
+      s[r] = pr * (dp[r] - dd);
+    }
+#pragma unroll
+    for (int j = 0; j < C::NJ; ++j) {
+      F b;
+      if constexpr (C::KP == 1) {
+        b = s[j];
+      } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) b[t] = static_cast<T>(s[j * 8 + t]);
+      }
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt)
+        acc[dt] = M::mma(load_frag<T>(Kt + (dt * 32 + c) * C::TS + key_of_reg(j * C::KP, g), true), b, acc[dt]);
+    }
+  }
+  if (!row_ok) return;
+  T* out = static_cast<T*>(p.dq) + hoff + (int64_t)my_row * p.D;
+#pragma unroll
+  for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = dt * 32 + drow(r, g);
+      if (d < p.D) out[d] = static_cast<T>(acc[dt][r] * p.scale);
+    }
+}
+
+// ------------------------------------------------------------------ dk / dv
+template <typename T, int DP, int WAVES, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * WAVES) void bwd_dkdv_kernel(const BwdParams p) {
+  using C = BwdCfg<T, DP>;
+  using M = Mfma<T>;
+  typedef typename M::frag F;
+  constexpr int NT = 64 * WAVES, BN = 32 * WAVES;
+  __shared__ __attribute__((aligned(16))) T Qs[C::HALF ? C::TT * C::RS : 1];
+  __shared__ __attribute__((aligned(16))) T Gs[C::HALF ? C::TT * C::RS : 1];
+  __shared__ __attribute__((aligned(16))) T Qt[DP * C::TS];
+  __shared__ __attribute__((aligned(16))) T Gt[DP * C::TS];
+  __shared__ float lse_s[C::TT], dd_s[C::TT];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int bh = blockIdx.y;
+  const int wg_key0 = blockIdx.x * BN;
+  const int key0 = wg_key0 + wave * 32;
+  const int my_key = key0 + c;
+  const bool key_ok = my_key < p.N;
+  const int64_t hoff = (int64_t)bh * p.N * p.D;
+  const T* Q = static_cast<const T*>(p.q) + hoff;
+  const T* K = static_cast<const T*>(p.k) + hoff;
+  const T* V = static_cast<const T*>(p.v) + hoff;
+  const T* dO = static_cast<const T*>(p.dout) + hoff;
+  const int bi = bh / p.H, hi = bh % p.H;
+
+  F kf[C::NKK], vf[C::NKK];
+  const int ksafe = key_ok ? my_key : 0;
+#pragma unroll
+  for (int kk = 0; kk < C::NKK; ++kk) {
+    const int d0 = kk * C::KSTEP + g * C::KP;
+    kf[kk] = load_frag<T>(K + (int64_t)ksafe * p.D + d0, key_ok && d0 < p.D);
+    vf[kk] = load_frag<T>(V + (int64_t)ksafe * p.D + d0, key_ok && d0 < p.D);
+  }
+  f32x16 dk[C::NDT], dv[C::NDT];
+#pragma unroll
+  for (int dt = 0; dt < C::NDT; ++dt) {
+    dk[dt] = f32x16{};
+    dv[dt] = f32x16{};
+  }
+  const int r_begin = p.causal ? (wg_key0 / C::TT) * C::TT : 0;
+
+  for (int t0 = r_begin; t0 < p.N; t0 += C::TT) {
+    __syncthreads();
+    stage_tile<T, DP, NT, C::HALF, true>(Q, t0, p.N, p.D, Qs, Qt, tid);
+    stage_tile<T, DP, NT, C::HALF, true>(dO, t0, p.N, p.D, Gs, Gt, tid);
+    if (tid < C::TT) {
+      const int ra = t0 + tid;
+      lse_s[tid] = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : kNegInf;
+      dd_s[tid] = ra < p.N ? p.d_row[(int64_t)bh * p.N + ra] : 0.f;
+    }
+    __syncthreads();
+    f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < C::NKK; ++kk) {
+      s = M::mma(a_frag<T, DP>(Qs, Qt, c, g, kk), kf[kk], s);
+      dp = M::mma(a_frag<T, DP>(Gs, Gt, c, g, kk), vf[kk], dp);
+    }
+    f32x16 pv;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int rl = key_of_reg(r, g);
+      const int row = t0 + rl;
+      const float lse = lse_s[rl];
+      bool ok = key_ok && row < p.N && lse > kNegInf;
+      if (p.causal) ok = ok && row >= my_key;
+      float x = s[r] * p.scale_log2;
+      if constexpr (HAS_BIAS) x = ok ? fmaf(load_bias_b(p.bias, bi, hi, row, my_key), kLog2e, x) : x;
+      const float pr = ok ? fast_exp2(x - lse) : 0.f;
+      pv[r] = pr;
+      s[r] = pr * (dp[r] - dd_s[rl]);
+    }
+#pragma unroll
+    for (int j = 0; j < C::NJ; ++j) {
+      F bp, bs;
+      if constexpr (C::KP == 1) {
+        bp = pv[j];
+        bs = s[j];
+      } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          bp[t] = static_cast<T>(pv[j * 8 + t]);
+          bs[t] = static_cast<T>(s[j * 8 + t]);
+        }
+      }
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt) {
+        const int off = (dt * 32 + c) * C::TS + key_of_reg(j * C::KP, g);
+        dv[dt] = M::mma(load_frag<T>(Gt + off, true), bp, dv[dt]);
+        dk[dt] = M::mma(load_frag<T>(Qt + off, true), bs, dk[dt]);
+      }
+    }
+  }
+  if (!key_ok) return;
+  T* okp = static_cast<T*>(p.dk) + hoff + (int64_t)my_key * p.D;
+  T* ovp = static_cast<T*>(p.dv) + hoff + (int64_t)my_key * p.D;
+#pragma unroll
+  for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = dt * 32 + drow(r, g);
+      if (d < p.D) {
+        okp[d] = static_cast<T>(dk[dt][r] * p.scale);
+        ovp[d] = static_cast<T>(dv[dt][r]);
+      }
+    }
+}
+
+// ------------------------------------------------------------------ row stats
+template <typename T, int DP, int WAVES, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * WAVES) void row_stats_kernel(const BwdParams p, float* row_m, float* row_z) {
+  using C = BwdCfg<T, DP>;
+  using M = Mfma<T>;
+  typedef typename M::frag F;
+  constexpr int NT = 64 * WAVES, BM = 32 * WAVES;
+  __shared__ __attribute__((aligned(16))) T Ks[C::HALF ? C::TT * C::RS : 1];
+  __shared__ __attribute__((aligned(16))) T Kt[C::HALF ? 1 : DP * C::TS];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int bh = blockIdx.y;
+  const int wg_row0 = blockIdx.x * BM;
+  const int wg_last = min(p.N, wg_row0 + BM) - 1;
+  const int my_row = wg_row0 + wave * 32 + c;
+  const bool row_ok = my_row < p.N;
+  const int64_t hoff = (int64_t)bh * p.N * p.D;
+  const T* Q = static_cast<const T*>(p.q) + hoff;
+  const T* K = static_cast<const T*>(p.k) + hoff;
+  const int bi = bh / p.H, hi = bh % p.H;
+  F qf[C::NKK];
+#pragma unroll
+  for (int kk = 0; kk < C::NKK; ++kk) {
+    const int d0 = kk * C::KSTEP + g * C::KP;
+    qf[kk] = load_frag<T>(Q + (int64_t)(row_ok ? my_row : 0) * p.D + d0, row_ok && d0 < p.D);
+  }
+  float m_run = kNegInf, z_lane = 0.f;
+  const int k_end = p.causal ? wg_last + 1 : p.N;
+  for (int t0 = 0; t0 < k_end; t0 += C::TT) {
+    __syncthreads();
+    stage_tile<T, DP, NT, C::HALF, !C::HALF>(K, t0, k_end, p.D, Ks, Kt, tid);
+    __syncthreads();
+    f32x16 s = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < C::NKK; ++kk) s = M::mma(a_frag<T, DP>(Ks, Kt, c, g, kk), qf[kk], s);
+    float mx = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = t0 + key_of_reg(r, g);
+      const bool ok = row_ok && key < k_end && (!p.causal || key <= my_row);
+      float x = s[r] * p.scale_log2;
+      if constexpr (HAS_BIAS) x = ok ? fmaf(load_bias_b(p.bias, bi, hi, my_row, key), kLog2e, x) : x;
+      s[r] = ok ? x : kNegInf;
+      mx = fmaxf(mx, s[r]);
+    }
+    mx = wave_max_pair(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == kNegInf ? 0.f : m_new;
+    float zs = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) zs += fast_exp2(s[r] - m_use);
+    z_lane = fmaf(z_lane, fast_exp2(m_run - m_use), zs);
+    m_run = m_new;
+  }
+  const float z = wave_sum_pair(z_lane);
+  if (row_ok && g == 0) {
+    row_m[(int64_t)bh * p.N + my_row] = z > 0.f ? m_run : kNegInf;
+    row_z[(int64_t)bh * p.N + my_row] = z;
+  }
+}
+
+// ------------------------------------------------------------------ dbias
+// One wave per 32x32 (row, key) tile of one (b', h'); operands straight from HBM.
+template <typename T, int DP>
+__global__ __launch_bounds__(64) void dbias_kernel(const BwdParams p, float* dbias, int bias_batch, int bias_heads) {
+  using C = BwdCfg<T, DP>;
+  using M = Mfma<T>;
+  const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
+  const int tiles = (p.N + 31) / 32;
+  const int ti = blockIdx.x / tiles, tj = blockIdx.x % tiles;
+  const int hb = blockIdx.y, bb = blockIdx.z;
+  const int my_row = ti * 32 + c;
+  const int krow = tj * 32 + swap23(c);  // key loaded by this lane for the A operand
+  const bool row_ok = my_row < p.N, krow_ok = krow < p.N;
+  const int B = p.BH / p.H;
+  const int b_lo = bias_batch == 1 ? 0 : bb, b_hi = bias_batch == 1 ? B : bb + 1;
+  const int h_lo = bias_heads == 1 ? 0 : hb, h_hi = bias_heads == 1 ? p.H : hb + 1;
+  f32x16 acc = f32x16{};
+  for (int b = b_lo; b < b_hi; ++b)
+    for (int h = h_lo; h < h_hi; ++h) {
+      const int bh = b * p.H + h;
+      const int64_t hoff = (int64_t)bh * p.N * p.D;
+      const T* Q = static_cast<const T*>(p.q) + hoff;
+      const T* K = static_cast<const T*>(p.k) + hoff;
+      const T* V = static_cast<const T*>(p.v) + hoff;
+      const T* dO = static_cast<const T*>(p.dout) + hoff;
+      f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < C::NKK; ++kk) {
+        const int d0 = kk * C::KSTEP + g * C::KP;
+        const bool dok = d0 < p.D;
+        const auto qb = load_frag<T>(Q + (int64_t)(row_ok ? my_row : 0) * p.D + d0, row_ok && dok);
+        const auto gb = load_frag<T>(dO + (int64_t)(row_ok ? my_row : 0) * p.D + d0, row_ok && dok);
+        const auto ka = load_frag<T>(K + (int64_t)(krow_ok ? krow : 0) * p.D + d0, krow_ok && dok);
+        const auto va = load_frag<T>(V + (int64_t)(krow_ok ? krow : 0) * p.D + d0, krow_ok && dok);
+        s = M::mma(ka, qb, s);
+        dp = M::mma(va, gb, dp);
+      }
+      const float lse = row_ok ? p.lse_row[(int64_t)bh * p.N + my_row] : kNegInf;
+      const float dd = row_ok ? p.d_row[(int64_t)bh * p.N + my_row] : 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = tj * 32 + key_of_reg(r, g);
+        bool ok = row_ok && key < p.N && lse > kNegInf && (!p.causal || key <= my_row);
+        const float x = ok ? fmaf(load_bias_b(p.bias, b, h, my_row, key), kLog2e, s[r] * p.scale_log2) : 0.f;
+        const float pr = ok ? fast_exp2(x - lse) : 0.f;
+        acc[r] += pr * (dp[r] - dd);
+      }
+    }
+  if (!row_ok) return;
+  float* outp = dbias + (((int64_t)bb * bias_heads + hb) * p.N + my_row) * p.N;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int key = tj * 32 + key_of_reg(r, g);
+    if (key < p.N) outp[key] = acc[r];
+  }
+}
+
+// ------------------------------------------------------------------ launchers
+template <typename T>
+static hipError_t pre_launch(const BwdParams& p, hipStream_t st) {
+  const int64_t rows = (int64_t)p.BH * p.N;
+  hipLaunchKernelGGL(bwd_pre_kernel<T>, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename T, int DP, bool B>
+static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
+  constexpr int W = 4;
+  hipError_t e = hipSuccess;
+  const dim3 grid((p.N + 32 * W - 1) / (32 * W), p.BH);
+  if (stage < 0 || stage == 0) {
+    if ((e = pre_launch<T>(p, st)) != hipSuccess) return e;
+  }
+  if (stage < 0 || stage == 1) {
+    hipLaunchKernelGGL((bwd_dq_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (stage < 0 || stage == 2) {
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+template <typename T, int DP>
+static hipError_t bwd_launch2(const BwdParams& p, int stage, hipStream_t st) {
+  return p.bias.ptr ? bwd_launch3<T, DP, true>(p, stage, st) : bwd_launch3<T, DP, false>(p, stage, st);
+}
+
+template <typename T>
+static hipError_t bwd_launch1(const BwdParams& p, int stage, hipStream_t st) {
+  switch (pad_head_dim(p.D)) {
+    case 32: return bwd_launch2<T, 32>(p, stage, st);
+    case 64: return bwd_launch2<T, 64>(p, stage, st);
+    default: return bwd_launch2<T, 128>(p, stage, st);
+  }
+}
+
+hipError_t launch_bwd(const BwdParams& p, int dtype, int stage, hipStream_t st) {
+  if (dtype == ELSA_F16) return bwd_launch1<f16>(p, stage, st);
+  if (dtype == ELSA_BF16) return bwd_launch1<bf16>(p, stage, st);
+  return bwd_launch1<float>(p, stage, st);
+}
+
+template <typename T, int DP>
+static hipError_t rs_launch2(const BwdParams& p, float* m, float* z, hipStream_t st) {
+  constexpr int W = 4;
+  const dim3 grid((p.N + 32 * W - 1) / (32 * W), p.BH);
+  if (p.bias.ptr)
+    hipLaunchKernelGGL((row_stats_kernel<T, DP, W, true>), grid, dim3(64 * W), 0, st, p, m, z);
+  else
+    hipLaunchKernelGGL((row_stats_kernel<T, DP, W, false>), grid, dim3(64 * W), 0, st, p, m, z);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t rs_launch1(const BwdParams& p, float* m, float* z, hipStream_t st) {
+  switch (pad_head_dim(p.D)) {
+    case 32: return rs_launch2<T, 32>(p, m, z, st);
+    case 64: return rs_launch2<T, 64>(p, m, z, st);
+    default: return rs_launch2<T, 128>(p, m, z, st);
+  }
+}
+
+hipError_t launch_row_stats(const BwdParams& p, float* row_m, float* row_z, int dtype, hipStream_t st) {
+  if (dtype == ELSA_F16) return rs_launch1<f16>(p, row_m, row_z, st);
+  if (dtype == ELSA_BF16) return rs_launch1<bf16>(p, row_m, row_z, st);
+  return rs_launch1<float>(p, row_m, row_z, st);
+}
+
+template <typename T, int DP>
+static hipError_t db_launch2(const BwdParams& p, float* dbias, int bb, int hb, hipStream_t st) {
+  hipError_t e = pre_launch<T>(p, st);
+  if (e != hipSuccess) return e;
+  const int tiles = (p.N + 31) / 32;
+  const dim3 grid(tiles * tiles, hb, bb);
+  hipLaunchKernelGGL((dbias_kernel<T, DP>), grid, dim3(64), 0, st, p, dbias, bb, hb);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t db_launch1(const BwdParams& p, float* dbias, int bb, int hb, hipStream_t st) {
+  switch (pad_head_dim(p.D)) {
+    case 32: return db_launch2<T, 32>(p, dbias, bb, hb, st);
+    case 64: return db_launch2<T, 64>(p, dbias, bb, hb, st);
+    default: return db_launch2<T, 128>(p, dbias, bb, hb, st);
+  }
+}
+
+hipError_t launch_dbias(const BwdParams& p, float* dbias, int bias_batch, int bias_heads, int dtype, hipStream_t st) {
+  if (dtype == ELSA_F16) return db_launch1<f16>(p, dbias, bias_batch, bias_heads, st);
+  if (dtype == ELSA_BF16) return db_launch1<bf16>(p, dbias, bias_batch, bias_heads, st);
+  return db_launch1<float>(p, dbias, bias_batch, bias_heads, st);
+}
+
+}  // namespace elsa

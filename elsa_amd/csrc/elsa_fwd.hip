@@ -1,0 +1,461 @@
+// ELSA forward on gfx950: Phase 1 (per-K-partition monoid fold on MFMA) and
+// Phase 2 (per-row up-sweep merge of the partition summaries read back from HBM).
+//
+// Phase 1 (replaces the Triton summary kernels of the reference,
+// attention_parallel_scan.py:123-372 and attention.py:22-106):
+//   one workgroup = 32*WAVES query rows of one head x one K partition.
+//   Each wave owns a 32-row tile and computes S^T = K Q^T on 32x32 MFMA tiles
+//   (Q^T fragments live in registers for the whole partition, K tiles come from
+//   LDS), folds the running (m, z) in registers, and accumulates
+//   O^T = V^T P^T with V^T staged transposed in LDS.  Because the A operand rows
+//   of K are permuted by swap23, the D-layout registers of S^T are already the
+//   B operand of the P^T product: no LDS round trip for P.
+//   Masked keys (>= partition end, or > row when causal) score -inf; a row with
+//   no valid key keeps the identity summary (-inf, 0, 0) (attention.py:91-100).
+//   The running max is exact per 64-key stage; the O rescale is skipped when
+//   no row of the wave raised its max.
+//
+// Phase 2 (replaces paper_scan_d64_kernel.cu:10-96 and the Triton up-sweep /
+// Hillis-Steele / finalize kernels, attention_parallel_scan.py:13-120, :375-415):
+//   one thread = one row x 8 head-dim elements; partition summaries are merged
+//   pairwise level by level in registers (Blelloch up-sweep order with identity
+//   padding, groups of 8 partitions), then out = s/z with the z>0 guard and the
+//   base-2 row state is stored.  For causal attention only partitions that start
+//   at or before the row are read: later ones are the identity, so this is the
+//   inclusive prefix at the row's own partition (the value the reference's
+//   Hillis-Steele scan hands to its finalize, attention_parallel_scan.py:745).
+#include "elsa_internal.h"
+#include "elsa_mfma.h"
+
+namespace elsa {
+
+int pad_head_dim(int d) { return d <= 32 ? 32 : (d <= 64 ? 64 : 128); }
+
+template <typename T, int DP>
+struct FwdCfg {
+  static constexpr int KP = Mfma<T>::KP;
+  static constexpr int KSTEP = 2 * KP;  // contraction length of one MFMA
+  static constexpr int NKK = DP / KSTEP;
+  static constexpr bool HALF = sizeof(T) == 2;
+  static constexpr int KT = ((HALF && DP == 128) || (!HALF && DP >= 64)) ? 32 : 64;  // keys per LDS stage
+  static constexpr int NSUB = KT / 32;
+  static constexpr int KPAD = HALF ? 8 : 1;
+  static constexpr int VPAD = HALF ? 8 : 1;
+  static constexpr int KS = DP + KPAD;  // LDS row stride of K   [KT][KS]
+  static constexpr int VS = KT + VPAD;  // LDS row stride of V^T [DP][VS]
+  static constexpr int LDS_ONE = (KT * KS + DP * VS) * (int)sizeof(T);
+  static constexpr int NBUF = (2 * LDS_ONE <= 98304) ? 2 : 1;
+  static constexpr int NDT = DP / 32;  // 32-wide head-dim tiles of O^T
+  static constexpr int NJ = 16 / KP;   // P^T.V^T MFMAs per 32-key sub-tile
+  static constexpr int CE = 16 / (int)sizeof(T);
+};
+
+int phase1_key_tile(int dtype, int dp) {
+  if (dtype == ELSA_F32) return dp >= 64 ? 32 : 64;
+  return dp == 128 ? 32 : 64;
+}
+
+__device__ inline float load_bias(const BiasView& b, int bi, int hi, int row, int key) {
+  const int64_t off = (int64_t)bi * b.sb + (int64_t)hi * b.sh + (int64_t)row * b.sq + (int64_t)key * b.sk;
+  if (b.dtype == ELSA_F32) return static_cast<const float*>(b.ptr)[off];
+  if (b.dtype == ELSA_F16) return static_cast<float>(static_cast<const f16*>(b.ptr)[off]);
+  return static_cast<float>(static_cast<const bf16*>(b.ptr)[off]);
+}
+
+__device__ inline void store4(void* base, int64_t off, int dtype, float a, float b, float c, float d) {
+  if (dtype == ELSA_F32) {
+    f32x4 v = {a, b, c, d};
+    *reinterpret_cast<f32x4*>(static_cast<float*>(base) + off) = v;
+  } else if (dtype == ELSA_F16) {
+    typedef f16 h4 __attribute__((ext_vector_type(4)));
+    h4 v = {(f16)a, (f16)b, (f16)c, (f16)d};
+    *reinterpret_cast<h4*>(static_cast<f16*>(base) + off) = v;
+  } else {
+    typedef bf16 b4 __attribute__((ext_vector_type(4)));
+    b4 v = {(bf16)a, (bf16)b, (bf16)c, (bf16)d};
+    *reinterpret_cast<b4*>(static_cast<bf16*>(base) + off) = v;
+  }
+}
+
+template <typename T, int DP, int WAVES, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p) {
+  using C = FwdCfg<T, DP>;
+  using M = Mfma<T>;
+  typedef typename M::frag F;
+  constexpr int NT = 64 * WAVES;
+  constexpr int BM = 32 * WAVES;
+  constexpr int CPR = DP / C::CE;  // 16-byte chunks per key row
+  static_assert((C::KT * CPR) % NT == 0, "staging must divide evenly");
+  constexpr int NCH = C::KT * CPR / NT;
+
+  __shared__ __attribute__((aligned(16))) T Ks[C::NBUF][C::KT * C::KS];
+  __shared__ __attribute__((aligned(16))) T Vt[C::NBUF][DP * C::VS];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int bh = blockIdx.y, kb = blockIdx.z;
+  const int q_end = p.q_start + p.q_len;
+  const int wg_row0 = p.q_start + blockIdx.x * BM;
+  const int wg_last = min(q_end, wg_row0 + BM) - 1;
+  const int k_begin = kb * p.part_len;
+  int k_end = min(p.N, k_begin + p.part_len);
+  if (p.causal) k_end = min(k_end, wg_last + 1);
+  if (k_begin >= k_end) return;  // every row of this workgroup sees the identity here
+
+  const int row0 = wg_row0 + wave * 32;
+  const int my_row = row0 + c;
+  const bool row_ok = my_row < q_end;
+  const int64_t hoff = (int64_t)bh * p.N * p.D;
+  const T* __restrict__ Q = static_cast<const T*>(p.q) + hoff;
+  const T* __restrict__ K = static_cast<const T*>(p.k) + hoff;
+  const T* __restrict__ V = static_cast<const T*>(p.v) + hoff;
+  const int bi = bh / p.H, hi = bh - (bh / p.H) * p.H;
+
+  // Q^T fragments (B operand of S^T = K Q^T): lane (c, g) holds Q[row c][d = kk*KSTEP + g*KP + t].
+  F qf[C::NKK];
+#pragma unroll
+  for (int kk = 0; kk < C::NKK; ++kk) {
+    const int d0 = kk * C::KSTEP + g * C::KP;
+    qf[kk] = load_frag<T>(Q + (int64_t)(row_ok ? my_row : 0) * p.D + d0, row_ok && d0 < p.D);
+  }
+
+  Chunk16 kreg[NCH], vreg[NCH];
+  auto gload = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int ci = tid + i * NT;
+      const int key = ci / CPR, d0 = (ci % CPR) * C::CE;
+      const int ka = t0 + key;
+      if (ka < k_end && d0 < p.D) {
+        const int64_t off = (int64_t)ka * p.D + d0;
+        kreg[i] = *reinterpret_cast<const Chunk16*>(K + off);
+        vreg[i] = *reinterpret_cast<const Chunk16*>(V + off);
+      } else {
+        kreg[i] = Chunk16{};
+        vreg[i] = Chunk16{};
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int ci = tid + i * NT;
+      const int key = ci / CPR, d0 = (ci % CPR) * C::CE;
+      T* kd = &Ks[buf][key * C::KS + d0];
+      if constexpr (C::HALF) {
+        *reinterpret_cast<Chunk16*>(kd) = kreg[i];
+      } else {
+        const T* src = reinterpret_cast<const T*>(&kreg[i]);
+#pragma unroll
+        for (int e = 0; e < C::CE; ++e) kd[e] = src[e];
+      }
+      const T* vs = reinterpret_cast<const T*>(&vreg[i]);
+#pragma unroll
+      for (int e = 0; e < C::CE; ++e) Vt[buf][(d0 + e) * C::VS + key] = vs[e];
+    }
+  };
+
+  f32x16 oacc[C::NDT];
+#pragma unroll
+  for (int dt = 0; dt < C::NDT; ++dt) oacc[dt] = f32x16{};
+  float m_run = kNegInf, z_lane = 0.f;
+  const float cs = p.scale_log2;
+  const int ntiles = (k_end - k_begin + C::KT - 1) / C::KT;
+
+  gload(k_begin);
+  sstore(0);
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = (C::NBUF == 2) ? (it & 1) : 0;
+    const int t0 = k_begin + it * C::KT;
+    const bool has_next = it + 1 < ntiles;
+    if (C::NBUF == 2 && has_next) gload(t0 + C::KT);
+    const T* ks = Ks[buf];
+    const T* vt = Vt[buf];
+
+    // S^T = K Q^T : lane (c, g) register r <-> key t0 + 32*sub + key_of_reg(r, g), row c.
+    f32x16 s[C::NSUB];
+#pragma unroll
+    for (int sub = 0; sub < C::NSUB; ++sub) {
+      s[sub] = f32x16{};
+      const T* krow = ks + (sub * 32 + swap23(c)) * C::KS + g * C::KP;
+#pragma unroll
+      for (int kk = 0; kk < C::NKK; ++kk) s[sub] = M::mma(load_frag<T>(krow + kk * C::KSTEP, true), qf[kk], s[sub]);
+    }
+
+    float mx = kNegInf;
+    if constexpr (HAS_BIAS) {
+#pragma unroll
+      for (int sub = 0; sub < C::NSUB; ++sub)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = t0 + sub * 32 + key_of_reg(r, g);
+          const bool ok = row_ok && key < k_end && (!p.causal || key <= my_row);
+          const float x = ok ? fmaf(s[sub][r], cs, load_bias(p.bias, bi, hi, my_row, key) * p.bias_log2) : kNegInf;
+          s[sub][r] = x;
+          mx = fmaxf(mx, x);
+        }
+    } else {
+      const bool need_mask = (t0 + C::KT > k_end) || (p.causal && (t0 + C::KT - 1 > row0));
+      if (need_mask) {
+#pragma unroll
+        for (int sub = 0; sub < C::NSUB; ++sub)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = t0 + sub * 32 + key_of_reg(r, g);
+            const bool ok = key < k_end && (!p.causal || key <= my_row);
+            if (!ok) s[sub][r] = kNegInf;
+          }
+      }
+#pragma unroll
+      for (int sub = 0; sub < C::NSUB; ++sub)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[sub][r], s[sub][r + 1]));
+    }
+    mx = wave_max_pair(mx);
+    const float m_tile = HAS_BIAS ? mx : mx * cs;
+    const float m_new = fmaxf(m_run, m_tile);
+    const float m_use = (m_new == kNegInf) ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - m_use);
+    float zs = 0.f;
+#pragma unroll
+    for (int sub = 0; sub < C::NSUB; ++sub)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = HAS_BIAS ? fast_exp2(s[sub][r] - m_use) : fast_exp2(fmaf(s[sub][r], cs, -m_use));
+        s[sub][r] = pr;
+        zs += pr;
+      }
+    z_lane = fmaf(z_lane, alpha, zs);
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+    }
+    m_run = m_new;
+
+    // O^T += V^T P^T : A = V^T rows d, B = P^T straight from the S^T registers.
+#pragma unroll
+    for (int sub = 0; sub < C::NSUB; ++sub)
+#pragma unroll
+      for (int j = 0; j < C::NJ; ++j) {
+        F b;
+        if constexpr (C::KP == 1) {
+          b = s[sub][j];
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; ++t) b[t] = static_cast<T>(s[sub][j * 8 + t]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt) {
+          const T* vrow = vt + (dt * 32 + c) * C::VS + sub * 32 + key_of_reg(j * C::KP, g);
+          oacc[dt] = M::mma(load_frag<T>(vrow, true), b, oacc[dt]);
+        }
+      }
+
+    if constexpr (C::NBUF == 2) {
+      if (has_next) sstore(buf ^ 1);
+      __syncthreads();
+    } else {
+      __syncthreads();
+      if (has_next) {
+        gload(t0 + C::KT);
+        sstore(0);
+        __syncthreads();
+      }
+    }
+  }
+
+  const float z = wave_sum_pair(z_lane);
+  if (!row_ok) return;
+  const int64_t ridx = ((int64_t)kb * p.BH + bh) * p.rows_pad + (my_row - p.q_start);
+  if (g == 0) {
+    p.m_buf[ridx] = m_run;
+    p.z_buf[ridx] = z;
+  }
+#pragma unroll
+  for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = dt * 32 + q4 * 8 + 4 * g;
+      if (d < p.D)
+        store4(p.s_buf, ridx * p.D + d, p.s_dtype, oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
+               oacc[dt][4 * q4 + 3]);
+    }
+}
+
+// ------------------------------------------------------------------ Phase 2
+template <typename ST>
+__device__ inline void load8(const void* base, int64_t off, float (&dst)[8]) {
+  const ST* ptr = static_cast<const ST*>(base) + off;
+  if constexpr (sizeof(ST) == 4) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(ptr);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(ptr + 4);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      dst[t] = a[t];
+      dst[t + 4] = b[t];
+    }
+  } else {
+    typedef ST v8 __attribute__((ext_vector_type(8)));
+    const v8 a = *reinterpret_cast<const v8*>(ptr);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) dst[t] = static_cast<float>(a[t]);
+  }
+}
+
+// (m, z, s) <- merge(a, b), attention_parallel_scan.py:55-60 / :111-116.
+__device__ inline void mono_merge(float ma, float za, const float (&sa)[8], float mb, float zb, const float (&sb)[8],
+                                  float& mo, float& zo, float (&so)[8]) {
+  const float m = fmaxf(ma, mb);
+  const float al = za > 0.f ? fast_exp2(ma - m) : 0.f;
+  const float be = zb > 0.f ? fast_exp2(mb - m) : 0.f;
+  float tmp[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) tmp[t] = fmaf(sa[t], al, sb[t] * be);
+  const float z = fmaf(za, al, zb * be);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) so[t] = tmp[t];
+  zo = z;
+  mo = z > 0.f ? m : kNegInf;
+}
+
+template <typename ST, typename TO>
+__global__ __launch_bounds__(256) void phase2_kernel(const Phase2Params p) {
+  const int cpr = p.D >> 3;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = (int64_t)p.BH * p.q_len * cpr;
+  if (gid >= total) return;
+  const int ch = (int)(gid % cpr);
+  const int64_t rl = gid / cpr;
+  const int r = (int)(rl % p.q_len);
+  const int bh = (int)(rl / p.q_len);
+  const int row = p.q_start + r;
+  int kb_hi = p.P - 1;
+  if (p.causal) kb_hi = min(kb_hi, row / p.part_len);
+
+  float am = kNegInf, az = 0.f, as[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) as[t] = 0.f;
+
+  for (int base = 0; base <= kb_hi; base += 8) {
+    float m[8], z[8], s[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int kb = base + i;
+      if (kb <= kb_hi) {
+        const int64_t idx = ((int64_t)kb * p.BH + bh) * p.rows_pad + r;
+        m[i] = p.m_buf[idx];
+        z[i] = p.z_buf[idx];
+        load8<ST>(p.s_buf, idx * p.D + ch * 8, s[i]);
+      } else {
+        m[i] = kNegInf;
+        z[i] = 0.f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) s[i][t] = 0.f;
+      }
+    }
+    // up-sweep: level widths 4, 2, 1; out[i] = merge(in[2i], in[2i+1])
+#pragma unroll
+    for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+      for (int i = 0; i < w; ++i) mono_merge(m[2 * i], z[2 * i], s[2 * i], m[2 * i + 1], z[2 * i + 1], s[2 * i + 1], m[i], z[i], s[i]);
+    mono_merge(am, az, as, m[0], z[0], s[0], am, az, as);
+  }
+
+  TO* out = static_cast<TO*>(p.out) + ((int64_t)bh * p.N + row) * p.D + ch * 8;
+  typedef TO o8 __attribute__((ext_vector_type(8)));
+  o8 ov;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) ov[t] = static_cast<TO>(az > 0.f ? as[t] / az : 0.f);
+  *reinterpret_cast<o8*>(out) = ov;
+  if (p.row_m != nullptr && ch == 0) {
+    p.row_m[(int64_t)bh * p.N + row] = az > 0.f ? am : kNegInf;
+    p.row_z[(int64_t)bh * p.N + row] = az;
+  }
+}
+
+// ------------------------------------------------------------------ launchers
+template <typename T, int DP, int W, bool B>
+static hipError_t launch1(const Phase1Params& p, hipStream_t st) {
+  const dim3 grid((p.q_len + 32 * W - 1) / (32 * W), p.BH, p.P);
+  hipLaunchKernelGGL((phase1_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename T, int DP>
+static hipError_t launch1_wb(const Phase1Params& p, int waves, hipStream_t st) {
+  const bool b = p.bias.ptr != nullptr;
+  if (waves == 2) return b ? launch1<T, DP, 2, true>(p, st) : launch1<T, DP, 2, false>(p, st);
+  return b ? launch1<T, DP, 4, true>(p, st) : launch1<T, DP, 4, false>(p, st);
+}
+
+template <typename T>
+static hipError_t launch1_d(const Phase1Params& p, int waves, hipStream_t st) {
+  switch (pad_head_dim(p.D)) {
+    case 32: return launch1_wb<T, 32>(p, waves, st);
+    case 64: return launch1_wb<T, 64>(p, waves, st);
+    default: return launch1_wb<T, 128>(p, waves, st);
+  }
+}
+
+hipError_t launch_phase1(const Phase1Params& p, int dtype, int waves, hipStream_t st) {
+  if (dtype == ELSA_F16) return launch1_d<f16>(p, waves, st);
+  if (dtype == ELSA_BF16) return launch1_d<bf16>(p, waves, st);
+  return launch1_d<float>(p, waves, st);
+}
+
+template <typename ST, typename TO>
+static hipError_t launch2(const Phase2Params& p, hipStream_t st) {
+  const int64_t total = (int64_t)p.BH * p.q_len * (p.D >> 3);
+  const dim3 grid((unsigned)((total + 255) / 256));
+  hipLaunchKernelGGL((phase2_kernel<ST, TO>), grid, dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename ST>
+static hipError_t launch2_o(const Phase2Params& p, hipStream_t st) {
+  if (p.out_dtype == ELSA_F16) return launch2<ST, f16>(p, st);
+  if (p.out_dtype == ELSA_BF16) return launch2<ST, bf16>(p, st);
+  return launch2<ST, float>(p, st);
+}
+
+hipError_t launch_phase2(const Phase2Params& p, hipStream_t st) {
+  if (p.s_dtype == ELSA_F16) return launch2_o<f16>(p, st);
+  if (p.s_dtype == ELSA_BF16) return launch2_o<bf16>(p, st);
+  return launch2_o<float>(p, st);
+}
+
+// ------------------------------------------------------------------ layout probe
+template <typename T>
+__global__ void debug_mfma_kernel(const T* a, const T* b, float* d) {
+  const int l = threadIdx.x;
+  typename Mfma<T>::frag fa, fb;
+  if constexpr (Mfma<T>::KP == 1) {
+    fa = a[l];
+    fb = b[l];
+  } else {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      fa[t] = a[l * 8 + t];
+      fb[t] = b[l * 8 + t];
+    }
+  }
+  f32x16 acc = Mfma<T>::mma(fa, fb, f32x16{});
+#pragma unroll
+  for (int r = 0; r < 16; ++r) d[l * 16 + r] = acc[r];
+}
+
+hipError_t launch_debug_mfma(int variant, const void* a, const void* b, float* d, hipStream_t st) {
+  if (variant == 0)
+    hipLaunchKernelGGL(debug_mfma_kernel<f16>, dim3(1), dim3(64), 0, st, (const f16*)a, (const f16*)b, d);
+  else if (variant == 1)
+    hipLaunchKernelGGL(debug_mfma_kernel<bf16>, dim3(1), dim3(64), 0, st, (const bf16*)a, (const bf16*)b, d);
+  else
+    hipLaunchKernelGGL(debug_mfma_kernel<float>, dim3(1), dim3(64), 0, st, (const float*)a, (const float*)b, d);
+  return hipGetLastError();
+}
+
+}  // namespace elsa

@@ -1,0 +1,91 @@
+// Internal launch interfaces shared by the kernel files and the C ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "elsa_hip.h"
+
+namespace elsa {
+
+// Phase-1 workgroup shape: 32 query rows per wave (one 32-row MFMA tile).
+constexpr int kRowsPerWave = 32;
+
+struct BiasView {
+  const void* ptr;
+  int dtype;
+  int64_t sb, sh, sq, sk;
+};
+
+// One Phase-1 launch covers query rows [q_start, q_start + q_len) of every head
+// and all K partitions.  Summaries are written to
+//   m[(kb * BH + bh) * rows_pad + r], z[...], s[((kb * BH + bh) * rows_pad + r) * D + d]
+// with r = row - q_start.
+struct Phase1Params {
+  const void* q;
+  const void* k;
+  const void* v;
+  BiasView bias;
+  float* m_buf;
+  float* z_buf;
+  void* s_buf;
+  int s_dtype;
+  int H, N, D, BH;
+  int q_start, q_len;
+  int part_len, P;
+  int causal;
+  float scale_log2;  // log2(e) / sqrt(D_model)
+  float bias_log2;   // log2(e)
+  int64_t rows_pad;
+};
+
+struct Phase2Params {
+  const float* m_buf;
+  const float* z_buf;
+  const void* s_buf;
+  int s_dtype;
+  void* out;
+  int out_dtype;
+  float* row_m;
+  float* row_z;
+  int N, D, BH;
+  int q_start, q_len;
+  int part_len, P;
+  int causal;
+  int64_t rows_pad;
+};
+
+// Launch helpers (return hipError_t of the launch).
+hipError_t launch_phase1(const Phase1Params& p, int dtype, int waves, hipStream_t stream);
+hipError_t launch_phase2(const Phase2Params& p, hipStream_t stream);
+int phase1_key_tile(int dtype, int head_dim_padded);
+int pad_head_dim(int d);
+
+struct BwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* out;
+  const void* dout;
+  const float* row_m;
+  const float* row_z;
+  void* dq;
+  void* dk;
+  void* dv;
+  BiasView bias;
+  float* d_row;    // [BH, N]
+  float* lse_row;  // [BH, N]
+  int H, N, D, BH;
+  int causal;
+  float scale;       // 1/sqrt(D_model)
+  float scale_log2;  // scale * log2(e)
+};
+
+// stage < 0: preprocess, dq and dk/dv; 0: preprocess only; 1: dq only; 2: dk/dv only.
+hipError_t launch_bwd(const BwdParams& p, int dtype, int stage, hipStream_t stream);
+hipError_t launch_row_stats(const BwdParams& p, float* row_m, float* row_z, int dtype, hipStream_t stream);
+hipError_t launch_dbias(const BwdParams& p, float* dbias, int bias_batch, int bias_heads, int dtype,
+                        hipStream_t stream);
+hipError_t launch_debug_mfma(int variant, const void* a, const void* b, float* d, hipStream_t stream);
+
+}  // namespace elsa

@@ -1,0 +1,116 @@
+// MFMA, fragment and LDS helpers for the ELSA HIP kernels (gfx950 / CDNA4 only).
+//
+// Every matrix product in this library is a 32x32 output tile on the wave64
+// matrix cores:
+//   fp16 : v_mfma_f32_32x32x16_f16   (A, B: 8 halves per lane, C/D: 16 floats)
+//   bf16 : v_mfma_f32_32x32x16_bf16  (A, B: 8 bf16 per lane,  C/D: 16 floats)
+//   fp32 : v_mfma_f32_32x32x2_f32    (A, B: 1 float per lane,  C/D: 16 floats)
+//
+// Operand layout (lane l, c = l % 32, g = l / 32, item t < KP):
+//   A[i][k] : lane with c == i holds k = g*KP + t        (row of A per lane)
+//   B[k][j] : lane with c == j holds k = g*KP + t        (column of B per lane)
+//   D[i][j] : lane with c == j, register r holds row i = (r/4)*8 + 4*g + (r%4)
+// Any assignment of k to (g, t) is valid as long as A and B use the same one;
+// the kernels exploit that freedom (see key_of_reg). The layout is checked on
+// the device by elsa_debug_mfma (tests/test_gpu_layout.py).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace elsa {
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<f16> {
+  static constexpr int KP = 8;
+  typedef f16x8 frag;
+  __device__ static inline f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<bf16> {
+  static constexpr int KP = 8;
+  typedef bf16x8 frag;
+  __device__ static inline f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<float> {
+  static constexpr int KP = 1;
+  typedef float frag;
+  __device__ static inline f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+};
+
+// Row of the 32x32 D tile held by register r of a lane in lane-group g.
+__device__ __host__ constexpr inline int drow(int r, int g) { return (r >> 2) * 8 + 4 * g + (r & 3); }
+
+// Permutation of the 32 rows of an A operand: swapping bits 2 and 3 of the row
+// position makes the D-layout register r of lane-group g correspond to key
+// 16*(r/8) + 8*g + (r%8) (key_of_reg), so a lane's 8 consecutive registers are
+// 8 consecutive keys and can feed the next MFMA's B operand directly.
+__device__ __host__ constexpr inline int swap23(int i) {
+  return (i & ~0xC) | ((i & 4) << 1) | ((i & 8) >> 1);
+}
+__device__ __host__ constexpr inline int key_of_reg(int r, int g) { return 16 * (r >> 3) + 8 * g + (r & 7); }
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <typename T>
+__device__ inline float to_f32(T x) { return static_cast<float>(x); }
+
+template <typename T>
+__device__ inline T from_f32(float x) { return static_cast<T>(x); }
+
+// Load KP elements (one MFMA operand fragment) from memory; `ok` false gives zeros.
+template <typename T>
+__device__ inline typename Mfma<T>::frag load_frag(const T* p, bool ok) {
+  typedef typename Mfma<T>::frag F;
+  if constexpr (Mfma<T>::KP == 1) {
+    return ok ? *p : 0.0f;
+  } else {
+    F z = {};
+    return ok ? *reinterpret_cast<const F*>(p) : z;
+  }
+}
+
+// Build a B-operand fragment of type T from KP consecutive fp32 registers.
+template <typename T, int R0>
+__device__ inline typename Mfma<T>::frag pack_frag(const f32x16& v) {
+  if constexpr (Mfma<T>::KP == 1) {
+    return v[R0];
+  } else {
+    typename Mfma<T>::frag f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) f[t] = static_cast<T>(v[R0 + t]);
+    return f;
+  }
+}
+
+// 16-byte raw chunk used for global->LDS staging.
+struct alignas(16) Chunk16 {
+  uint32_t w[4];
+};
+
+__device__ inline float wave_max_pair(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+__device__ inline float wave_sum_pair(float x) { return x + __shfl_xor(x, 32); }
+
+}  // namespace elsa

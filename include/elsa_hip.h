@@ -1,0 +1,158 @@
+/*
+ * elsa_hip.h -- C ABI of libelsa_hip.so, the MI355X (gfx950) implementation of
+ * ELSA two-pass exact monoid-scan attention.
+ *
+ * Conventions
+ *   - Every tensor is caller-allocated device memory, row-major and contiguous:
+ *     q, k, v, out, dout, dq, dk, dv are [B, H, N, D]; row state and the
+ *     backward's D/LSE2 rows are [B*H, N] fp32.  The library never allocates
+ *     device memory (callers size `workspace` with the *_plan / *_workspace_bytes
+ *     queries), so every entry point may be recorded into a hipGraph.
+ *   - Kernels are enqueued on `stream` (a hipStream_t passed as void*; NULL is
+ *     the default stream).  Calls return after enqueueing.
+ *   - Return 0 (ELSA_OK) or a negative elsa_status.  Nothing is thrown across
+ *     the ABI.  elsa_last_error() gives a thread-local message for the last
+ *     failing call on the calling thread.
+ *   - Row state is in the base-2 domain: row_m = max_k(s*log2(e)),
+ *     row_z = sum_k exp2(s*log2(e) - row_m) with s = q.k/sqrt(D) (+ bias);
+ *     rows without any valid key have row_m = -inf, row_z = 0 and out = 0.
+ *   - The library is stateless and re-entrant.
+ *
+ * Reference interfaces replaced (paths under the reference's
+ * src/elsa_twopass_clean/):
+ *   elsa_fwd         the forward orchestrators _twopass_attention_d64_parallel_final
+ *                    (attention_parallel_scan.py:443-584),
+ *                    twopass_attention_blelloch_final_scan (:762-961) and
+ *                    twopass_attention_hillis_steele_scan (:587-759).
+ *   elsa_phase1      the Phase-1 launches of the 5 Triton summary kernels
+ *                    (attention_parallel_scan.py:486-563, :680-708, :881-909;
+ *                    attention.py:22-106).
+ *   elsa_phase2      the pybind Phase-2 FFI final_reduce(m,z,s,out,row_m,row_z,
+ *                    q_start,n_ctx,k_blocks,q_blocks,bh,block_m,store_state)
+ *                    (cuda/paper_scan_d64.cpp:18-20, paper_scan_d64_cuda.py:37-67)
+ *                    and the Triton up-sweep / Hillis-Steele / finalize launches
+ *                    (attention_parallel_scan.py:710-753, :911-955).
+ *   elsa_bwd         twopass_attention_backward's launches of the preprocess,
+ *                    dq and dk/dv kernels (attention_bwd.py:765-838);
+ *                    elsa_bwd_stage issues one of them (:767, :786, :812).
+ *   elsa_row_stats   the _row_stats_kernel launch (attention_bwd.py:741-764).
+ *   elsa_dbias       the _dbias_dense_kernel launch (attention_bwd.py:926-971).
+ */
+#ifndef ELSA_HIP_H
+#define ELSA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ELSA_ABI_VERSION 1
+
+typedef enum elsa_dtype { ELSA_F16 = 0, ELSA_BF16 = 1, ELSA_F32 = 2 } elsa_dtype;
+
+typedef enum elsa_status {
+  ELSA_OK = 0,
+  ELSA_ERR_INVALID = -1,     /* bad shape, dtype, pointer or option           */
+  ELSA_ERR_WORKSPACE = -2,   /* workspace missing or smaller than required     */
+  ELSA_ERR_LAUNCH = -3,      /* HIP runtime / kernel launch error              */
+  ELSA_ERR_UNSUPPORTED = -4  /* valid request this build does not implement    */
+} elsa_status;
+
+/* Optional additive bias on the natural-log scores, broadcast by zero strides
+ * (attention.py:120-159).  Strides are in elements. */
+typedef struct elsa_bias_desc {
+  const void* ptr;      /* NULL: no bias                                       */
+  int32_t dtype;        /* elsa_dtype of the bias values                       */
+  int32_t _pad;
+  int64_t stride_b, stride_h, stride_q, stride_k;
+} elsa_bias_desc;
+
+typedef struct elsa_fwd_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  float* row_m;          /* [B*H, N] or NULL                                   */
+  float* row_z;          /* [B*H, N] or NULL (both or neither)                 */
+  elsa_bias_desc bias;
+  int32_t batch, heads, seq_len, head_dim;
+  int32_t dtype;         /* elsa_dtype of q, k, v, out                         */
+  int32_t summary_dtype; /* elsa_dtype of the Phase-1 s summaries in HBM       */
+  int32_t is_causal;
+  int32_t partition_len; /* keys per K partition (block_n); 0 = auto routing   */
+  int32_t q_chunk;       /* query rows per Phase1+Phase2 pass; 0 = auto        */
+  float scale;           /* softmax scale on q.k; 0 = 1/sqrt(head_dim)          */
+  void* workspace;
+  size_t workspace_bytes;
+} elsa_fwd_args;
+
+typedef struct elsa_fwd_plan {
+  int32_t partitions;    /* P: number of K partitions (Phase-1 summaries/row)  */
+  int32_t partition_len; /* keys per partition                                 */
+  int32_t q_chunk;       /* query rows per pass                                */
+  int32_t block_m;       /* query rows per Phase-1 workgroup                   */
+  int32_t key_tile;      /* keys per LDS stage inside a partition              */
+  int32_t _pad;
+  size_t workspace_bytes;
+} elsa_fwd_plan;
+
+typedef struct elsa_bwd_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* out;
+  const void* dout;
+  const float* row_m;    /* [B*H, N] forward row state (required)              */
+  const float* row_z;
+  void* dq;
+  void* dk;
+  void* dv;
+  elsa_bias_desc bias;
+  int32_t batch, heads, seq_len, head_dim;
+  int32_t dtype;
+  int32_t is_causal;
+  float scale;           /* softmax scale on q.k; 0 = 1/sqrt(head_dim)          */
+  int32_t _pad;
+  void* workspace;       /* 2*B*H*N floats (D and LSE2 rows)                   */
+  size_t workspace_bytes;
+} elsa_bwd_args;
+
+int elsa_abi_version(void);
+const char* elsa_last_error(void);
+/* sizeof of the argument structs as compiled into the library (ABI check). */
+size_t elsa_struct_size(int which); /* 0 fwd_args, 1 fwd_plan, 2 bwd_args, 3 bias_desc */
+
+/* Tiling, partition routing and workspace size for a forward call. */
+int elsa_fwd_plan_get(const elsa_fwd_args* args, elsa_fwd_plan* plan);
+/* Full forward: for each q-chunk, Phase 1 (summaries -> workspace) then Phase 2. */
+int elsa_fwd(const elsa_fwd_args* args, void* stream);
+/* The two passes separately, for rows [q_start, q_start+q_len) (q_len <= plan.q_chunk). */
+int elsa_phase1(const elsa_fwd_args* args, int32_t q_start, int32_t q_len, void* stream);
+int elsa_phase2(const elsa_fwd_args* args, int32_t q_start, int32_t q_len, void* stream);
+
+size_t elsa_bwd_workspace_bytes(const elsa_bwd_args* args);
+/* dq, dk, dv from the saved row state (exact recompute of p). */
+int elsa_bwd(const elsa_bwd_args* args, void* stream);
+/* One stage of elsa_bwd: 0 = D/LSE2 preprocess (into the workspace), 1 = dq kernel,
+ * 2 = dk/dv kernel (stages 1 and 2 read what stage 0 wrote); -1 = all three. */
+int elsa_bwd_stage(const elsa_bwd_args* args, int32_t stage, void* stream);
+/* Recompute the base-2 row state (row_m, row_z) from q, k (and bias). Uses
+ * args->q, k, bias, shape fields; writes row_m/row_z [B*H, N]. */
+int elsa_row_stats(const elsa_bwd_args* args, float* row_m, float* row_z, void* stream);
+/* dbias[b', h', i, j] = sum over broadcast (b, h) of p*(dp - D), fp32 output of
+ * shape [bias_batch, bias_heads, N, N] (bias_batch in {1,B}, bias_heads in {1,H}).
+ * Needs args->row_m/row_z and the bias descriptor. */
+int elsa_dbias(const elsa_bwd_args* args, float* dbias, int32_t bias_batch, int32_t bias_heads,
+               void* stream);
+
+/* Device check of the MFMA operand/result layout: variant 0 fp16, 1 bf16, 2 fp32.
+ * a, b: [64 lanes][KP] operand elements; d: [64 lanes][16] floats. */
+int elsa_debug_mfma(int32_t variant, const void* a, const void* b, float* d, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ELSA_HIP_H */

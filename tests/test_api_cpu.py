@@ -1,0 +1,157 @@
+"""CPU tests of the host side: the C ABI loads and exports what include/elsa_hip.h
+declares, struct layouts match, the planner routes as documented, invalid calls
+fail with a status and a message (no GPU needed: no kernel is launched), and the
+Python API raises the reference's ValueErrors."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from elsa_amd import _lib
+import elsa_amd
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_functions():
+    text = (ROOT / "include" / "elsa_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(elsa_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert set(declared) == set(_lib.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_struct_sizes():
+    lib = _lib.load()
+    assert lib.elsa_abi_version() == 1
+    for which, st in _lib._STRUCTS.items():
+        assert lib.elsa_struct_size(which) == ctypes.sizeof(st)
+
+
+def _args(n=16384, bh=(1, 8), d=64, dtype=_lib.ELSA_F16, causal=0, part=0, qc=0):
+    a = _lib.FwdArgs()
+    a.q = a.k = a.v = a.out = 1
+    a.batch, a.heads = bh
+    a.seq_len, a.head_dim = n, d
+    a.dtype = dtype
+    a.summary_dtype = dtype
+    a.is_causal = causal
+    a.partition_len = part
+    a.q_chunk = qc
+    return a
+
+
+def _plan(a):
+    lib = _lib.load()
+    p = _lib.FwdPlan()
+    rc = lib.elsa_fwd_plan_get(ctypes.byref(a), ctypes.byref(p))
+    return rc, p
+
+
+def test_plan_north_star_routing():
+    rc, p = _plan(_args())
+    assert rc == 0
+    assert p.partitions >= 2 and p.partitions * p.partition_len >= 16384
+    assert p.q_chunk == 16384 and p.block_m == 128 and p.key_tile == 64
+    rows = p.partitions * 8 * 16384
+    assert p.workspace_bytes >= rows * (8 + 64 * 2)
+
+
+@pytest.mark.parametrize("n,bh,d", [(49, (8, 3), 32), (197, (8, 3), 64), (1024, (1, 8), 64), (65536, (1, 8), 64),
+                                    (4097, (8, 3), 64), (300, (1, 2), 128)])
+def test_plan_partitions_cover_sequence(n, bh, d):
+    rc, p = _plan(_args(n=n, bh=bh, d=d))
+    assert rc == 0
+    assert p.partitions * p.partition_len >= n > (p.partitions - 1) * p.partition_len
+    assert p.q_chunk >= 1
+
+
+def test_plan_user_partition_and_chunk():
+    rc, p = _plan(_args(n=513, bh=(1, 2), part=128, qc=128))
+    assert rc == 0 and p.partition_len == 128 and p.partitions == 5 and p.q_chunk == 128
+
+
+@pytest.mark.parametrize("field,value,code", [("head_dim", 136, -1), ("head_dim", 20, -1), ("seq_len", 0, -1),
+                                              ("dtype", 7, -1), ("summary_dtype", 9, -1)])
+def test_plan_rejects_invalid(field, value, code):
+    a = _args()
+    setattr(a, field, value)
+    rc, _ = _plan(a)
+    assert rc == code
+    assert _lib.load().elsa_last_error().decode()
+
+
+def test_fwd_rejects_missing_workspace_without_launching():
+    lib = _lib.load()
+    a = _args(n=256, bh=(1, 1))
+    rc = lib.elsa_fwd(ctypes.byref(a), None)
+    assert rc == _lib.ELSA_ERR_WORKSPACE
+    assert "workspace" in lib.elsa_last_error().decode()
+    a.q = None
+    assert lib.elsa_fwd(ctypes.byref(a), None) == _lib.ELSA_ERR_INVALID
+
+
+def test_bwd_and_dbias_reject_bad_args_without_launching():
+    lib = _lib.load()
+    b = _lib.BwdArgs()
+    b.batch, b.heads, b.seq_len, b.head_dim, b.dtype = 1, 1, 64, 64, _lib.ELSA_F16
+    b.q = b.k = b.v = 1
+    assert lib.elsa_bwd(ctypes.byref(b), None) == _lib.ELSA_ERR_INVALID  # no out/dout/grads
+    b.out = b.dout = b.dq = b.dk = b.dv = b.row_m = b.row_z = 1
+    assert lib.elsa_bwd(ctypes.byref(b), None) == _lib.ELSA_ERR_WORKSPACE
+    assert lib.elsa_bwd_workspace_bytes(ctypes.byref(b)) >= 2 * 64 * 4
+    assert lib.elsa_dbias(ctypes.byref(b), 1, 2, 1, None) == _lib.ELSA_ERR_INVALID  # bias_batch 2 vs B=1
+    assert lib.elsa_debug_mfma(5, 1, 1, 1, None) == _lib.ELSA_ERR_INVALID
+
+
+def test_python_api_validation_on_cpu_tensors():
+    q = torch.zeros(1, 2, 8, 16)
+    with pytest.raises(ValueError, match="CUDA"):
+        elsa_amd.twopass_attention(q, q, q)
+    with pytest.raises(ValueError, match=r"\[B,H,N,D\]"):
+        elsa_amd.twopass_attention(q[0], q[0], q[0])
+    with pytest.raises(ValueError, match="identical shapes"):
+        elsa_amd.twopass_attention(q, q[:, :1], q)
+    with pytest.raises(ValueError, match="CUDA"):
+        elsa_amd.twopass_attention_with_state(q, q, q)
+    with pytest.raises(ValueError, match="CUDA"):
+        elsa_amd.twopass_attention_backward(q, q, q, q, q)
+    with pytest.raises(ValueError, match="identical shapes"):
+        elsa_amd.twopass_attention_backward(q, q, q, q, q[:, :1])
+
+
+def test_reference_defaults_and_warps_validation():
+    from elsa_amd.attention import _paper_scan_defaults, _validate_warps
+
+    assert _paper_scan_defaults(dtype=torch.float16, seq_len=16384, head_dim=64, block_m=None, block_n=None,
+                                q_chunk_size=None, phase1_warps=None, phase2_warps=None, phase1_stages=None,
+                                phase2_stages=None) == (64, 2048, 4096, 4, 4, 1, 1)
+    assert _paper_scan_defaults(dtype=torch.float32, seq_len=1000, head_dim=64, block_m=None, block_n=None,
+                                q_chunk_size=None, phase1_warps=None, phase2_warps=None, phase1_stages=None,
+                                phase2_stages=None)[:3] == (32, 1024, 1024)
+    with pytest.raises(ValueError, match="1, 2, 4, or 8"):
+        _validate_warps("phase1_warps", 3)
+
+
+def test_canonical_bias_cpu():
+    from elsa_amd.attention import _canonical_bias
+
+    dev = torch.device("cpu")
+    m = _canonical_bias(torch.zeros(3, 8, 8), batch=2, heads=3, seq_len=8, device=dev)
+    assert (m.stride_b, m.stride_h, m.stride_q, m.stride_k) == (0, 64, 8, 1)
+    m = _canonical_bias(torch.zeros(8, 8), batch=2, heads=3, seq_len=8, device=dev)
+    assert (m.stride_b, m.stride_h) == (0, 0)
+    with pytest.raises(ValueError, match="4D bias"):
+        _canonical_bias(torch.zeros(3, 3, 8, 8), batch=2, heads=3, seq_len=8, device=dev)
+    with pytest.raises(ValueError, match="last dims"):
+        _canonical_bias(torch.zeros(8, 7), batch=2, heads=3, seq_len=8, device=dev)

@@ -1,0 +1,140 @@
+"""GPU parity of the recompute backward (preprocess + dq kernel + dk/dv kernel), the
+row-stats recompute and dbias, through the C ABI, against the oracle and the fp64
+closed form.  Shapes follow the reference's tests/test_attention_bwd.py:15-46 and
+benchmarks/bwd_grad_correctness.py:11-34 (ViT odd lengths)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import elsa_amd
+from elsa_amd.attention_bwd import _dense_bias_backward
+from oracle import elsa_oracle as O
+from tests.gpu_util import GRAD_TOL, describe, dev, host, max_abs
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_train(q, k, v, do, dt, **kw):
+    qt, kt, vt = (dev(x, dt).requires_grad_(True) for x in (q, k, v))
+    out = elsa_amd.twopass_attention_train(qt, kt, vt, **kw)
+    out.backward(dev(do, dt))
+    torch.cuda.synchronize()
+    return out, qt.grad, kt.grad, vt.grad
+
+
+CASES = [
+    ((1, 2, 64, 32), "fp32", False),
+    ((1, 2, 64, 32), "fp32", True),
+    ((1, 2, 64, 32), "fp16", False),
+    ((1, 2, 64, 32), "fp16", True),
+    ((2, 3, 1025, 64), "fp32", False),
+    ((2, 3, 1025, 64), "fp16", False),
+    ((1, 2, 1025, 64), "fp16", True),
+    ((1, 2, 197, 64), "fp16", True),
+    ((1, 2, 4096, 64), "fp16", False),
+    ((1, 2, 4097, 64), "fp16", True),
+    ((1, 2, 300, 128), "fp16", False),
+    ((1, 2, 300, 128), "fp32", True),
+    ((1, 3, 197, 64), "bf16", False),
+    ((1, 2, 90, 40), "fp32", False),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-{c[1]}-{'causal' if c[2] else 'full'}" for c in CASES])
+def test_backward_matches_oracle_and_closed_form(case):
+    shape, dt, causal = case
+    describe(f"backward {case}")
+    q, k, v, do = O.make_inputs(shape, seed=2026 + shape[2], dtype=dt, with_dout=True, dout_scale=0.1)
+    out, dq, dk, dv = _run_train(q, k, v, do, dt, is_causal=causal)
+    qf, kf, vf, dof = (np.asarray(x, np.float32) for x in (q, k, v, do))
+    eq, ek, ev, _ = O.exact_backward(qf, kf, vf, dof, is_causal=causal)
+    tol = GRAD_TOL[dt]
+    for name, got, exp in (("dq", dq, eq), ("dk", dk, ek), ("dv", dv, ev)):
+        err = max_abs(host(got), exp)
+        assert err <= tol, (name, err)
+    if shape[-1] % 8 == 0 and dt != "bf16":
+        fo, fm, fz = O.forward(q, k, v, is_causal=causal, dtype=dt, mode="ref")
+        rq, rk, rv = O.backward(q, k, v, fo, do, fm, fz, is_causal=causal, dtype=dt, mode="ref")
+        for name, got, exp in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+            err = max_abs(host(got), exp)
+            assert err <= tol, (name, err)
+
+
+@pytest.mark.parametrize("dt", ["fp32", "fp16"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_reference_train_test_against_sdpa(dt, causal):
+    # tests/test_attention_bwd.py:15-46 (seed 11, q,k x0.5, dO x0.25, atol=rtol 2.5e-3 / 8e-2)
+    torch.manual_seed(11)
+    shape = (1, 2, 64, 32)
+    dtype = torch.float32 if dt == "fp32" else torch.float16
+    q = (torch.randn(shape, device="cuda", dtype=dtype) * 0.5).requires_grad_(True)
+    k = (torch.randn(shape, device="cuda", dtype=dtype) * 0.5).requires_grad_(True)
+    v = torch.randn(shape, device="cuda", dtype=dtype).requires_grad_(True)
+    dout = torch.randn(shape, device="cuda", dtype=dtype) * 0.25
+    q_ref, k_ref, v_ref = (t.detach().float().cpu().requires_grad_(True) for t in (q, k, v))
+    ref = torch.nn.functional.scaled_dot_product_attention(q_ref, k_ref, v_ref, is_causal=causal,
+                                                           scale=1.0 / shape[-1] ** 0.5)
+    ref.backward(dout.float().cpu())
+    out = elsa_amd.twopass_attention_train(q, k, v, is_causal=causal)
+    out.backward(dout)
+    tol = 2.5e-3 if dt == "fp32" else 8e-2
+    torch.testing.assert_close(out.float().cpu(), ref, atol=tol, rtol=tol)
+    for a, b in ((q.grad, q_ref.grad), (k.grad, k_ref.grad), (v.grad, v_ref.grad)):
+        torch.testing.assert_close(a.float().cpu(), b, atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("dt", ["fp32", "fp16"])
+def test_backward_without_saved_state_uses_row_stats(dt):
+    describe(f"backward row-stats {dt}")
+    q, k, v, do = O.make_inputs((1, 2, 333, 64), seed=4, dtype=dt, with_dout=True, dout_scale=0.1)
+    qd, kd, vd, dod = (dev(x, dt) for x in (q, k, v, do))
+    out, rm, rz = elsa_amd.twopass_attention_with_state(qd, kd, vd, is_causal=True)
+    g_state = elsa_amd.twopass_attention_backward(qd, kd, vd, out, dod, is_causal=True, row_m=rm, row_z=rz)
+    g_none = elsa_amd.twopass_attention_backward(qd, kd, vd, out, dod, is_causal=True)
+    for a, b in zip(g_state, g_none):
+        assert max_abs(host(a), host(b)) <= GRAD_TOL[dt]
+    from elsa_amd.attention_bwd import _row_stats
+    from elsa_amd.attention import _canonical_bias
+    m2, z2 = _row_stats(qd, kd, _canonical_bias(None, batch=1, heads=2, seq_len=333, device=qd.device),
+                        is_causal=True, scale=1 / 8)
+    _, em, ez = O.exact_forward(np.float32(q), np.float32(k), np.float32(v), is_causal=True)
+    assert np.abs(host(m2) - em).max() <= 1e-4 * np.abs(em).max()
+    np.testing.assert_allclose(host(z2), ez, rtol=1e-4 if dt == "fp32" else 2e-3)
+
+
+@pytest.mark.parametrize("dt", ["fp32", "fp16"])
+@pytest.mark.parametrize("bias_shape", [(1, 3, 49, 49), (4, 3, 49, 49), (49, 49), (3, 49, 49), (4, 1, 49, 49)])
+def test_bias_gradients(dt, bias_shape):
+    describe(f"backward bias {bias_shape} {dt}")
+    shape = (4, 3, 49, 32)
+    q, k, v, do = O.make_inputs(shape, seed=9, dtype=dt, with_dout=True, dout_scale=0.1)
+    bias = (np.random.default_rng(9).standard_normal(bias_shape) * 0.5).astype(np.float32)
+    qt, kt, vt = (dev(x, dt).requires_grad_(True) for x in (q, k, v))
+    bt = dev(bias, "fp32").requires_grad_(True)
+    out = elsa_amd.twopass_attention_train(qt, kt, vt, bias=bt)
+    out.backward(dev(do, dt))
+    torch.cuda.synchronize()
+    qf, kf, vf, dof = (np.asarray(x, np.float32) for x in (q, k, v, do))
+    eq, ek, ev, _ = O.exact_backward(qf, kf, vf, dof, bias=bias)
+    eo, em, ez = O.exact_forward(qf, kf, vf, bias=bias)
+    edb = O.dbias(qf, kf, vf, eo, dof, em, ez, bias=bias)
+    tol = GRAD_TOL[dt]
+    for got, exp in ((qt.grad, eq), (kt.grad, ek), (vt.grad, ev)):
+        assert max_abs(host(got), exp) <= tol
+    assert bt.grad.shape == bias.shape
+    summed = (shape[0] * shape[1]) // int(np.prod(bias_shape[:-2]))  # (b, h) pairs folded into each entry
+    assert max_abs(host(bt.grad), edb) <= 2 * tol * summed
+
+
+def test_dbias_causal_matches_closed_form():
+    describe("dbias causal")
+    q, k, v, do = O.make_inputs((2, 2, 70, 32), seed=12, dtype="fp32", with_dout=True, dout_scale=0.1)
+    bias = (np.random.default_rng(12).standard_normal((2, 2, 70, 70)) * 0.3).astype(np.float32)
+    qd, kd, vd, dod, bd = (dev(x, "fp32") for x in (q, k, v, do, bias))
+    out, rm, rz = elsa_amd.twopass_attention_with_state(qd, kd, vd, bias=bd, is_causal=True)
+    db = _dense_bias_backward(qd, kd, vd, out, dod, bias=bd, is_causal=True, row_m=rm, row_z=rz)
+    eo, em, ez = O.exact_forward(q, k, v, bias=bias, is_causal=True)
+    edb = O.dbias(q, k, v, eo, do, em, ez, bias=bias, is_causal=True)
+    assert max_abs(host(db), edb) <= 1e-6
