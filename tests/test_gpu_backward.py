@@ -11,7 +11,7 @@ import torch
 import elsa_amd
 from elsa_amd.attention_bwd import _dense_bias_backward
 from oracle import elsa_oracle as O
-from tests.gpu_util import GRAD_TOL, describe, dev, host, max_abs
+from tests.gpu_util import GRAD_TOL, assert_parity, describe, dev, host, max_abs
 
 pytestmark = pytest.mark.gpu
 
@@ -50,16 +50,10 @@ def test_backward_matches_oracle_and_closed_form(case):
     out, dq, dk, dv = _run_train(q, k, v, do, dt, is_causal=causal)
     qf, kf, vf, dof = (np.asarray(x, np.float32) for x in (q, k, v, do))
     eq, ek, ev, _ = O.exact_backward(qf, kf, vf, dof, is_causal=causal)
-    tol = GRAD_TOL[dt]
-    for name, got, exp in (("dq", dq, eq), ("dk", dk, ek), ("dv", dv, ev)):
-        err = max_abs(host(got), exp)
-        assert err <= tol, (name, err)
-    if shape[-1] % 8 == 0 and dt != "bf16":
-        fo, fm, fz = O.forward(q, k, v, is_causal=causal, dtype=dt, mode="ref")
-        rq, rk, rv = O.backward(q, k, v, fo, do, fm, fz, is_causal=causal, dtype=dt, mode="ref")
-        for name, got, exp in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
-            err = max_abs(host(got), exp)
-            assert err <= tol, (name, err)
+    fo, fm, fz = O.forward(q, k, v, is_causal=causal, dtype=dt, mode="ref")
+    rq, rk, rv = O.backward(q, k, v, fo, do, fm, fz, is_causal=causal, dtype=dt, mode="ref")
+    for name, got, exp, ref in (("dq", dq, eq, rq), ("dk", dk, ek, rk), ("dv", dv, ev, rv)):
+        describe(f"{name} {assert_parity(host(got), exp, ref, GRAD_TOL[dt], name)}")
 
 
 @pytest.mark.parametrize("dt", ["fp32", "fp16"])
@@ -121,8 +115,10 @@ def test_bias_gradients(dt, bias_shape):
     eo, em, ez = O.exact_forward(qf, kf, vf, bias=bias)
     edb = O.dbias(qf, kf, vf, eo, dof, em, ez, bias=bias)
     tol = GRAD_TOL[dt]
-    for got, exp in ((qt.grad, eq), (kt.grad, ek), (vt.grad, ev)):
-        assert max_abs(host(got), exp) <= tol
+    fo, fm, fz = O.forward(q, k, v, bias=bias, dtype=dt, mode="ref")
+    rq, rk, rv = O.backward(q, k, v, fo, do, fm, fz, bias=bias, dtype=dt, mode="ref")
+    for name, got, exp, ref in (("dq", qt.grad, eq, rq), ("dk", kt.grad, ek, rk), ("dv", vt.grad, ev, rv)):
+        assert_parity(host(got), exp, ref, tol, name)
     assert bt.grad.shape == bias.shape
     summed = (shape[0] * shape[1]) // int(np.prod(bias_shape[:-2]))  # (b, h) pairs folded into each entry
     assert max_abs(host(bt.grad), edb) <= 2 * tol * summed
