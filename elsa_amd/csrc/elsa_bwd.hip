@@ -298,6 +298,378 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dkdv_kernel(const BwdParams p)
     }
 }
 
+// ------------------------------------------------------------------ fp16 / bf16 dq and dk/dv
+// Same tiling ideas as the fp16/bf16 Phase 1: tiles are staged row-major with
+// 16-byte copies (double-buffered through registers) and transposed MFMA operands
+// (K^T for dq; Q^T, dO^T for dk/dv) come from the transposing LDS load.  RT (dq)
+// and KRT (dk/dv) are the 32-wide tiles per wave.
+template <typename T, int DP>
+struct HalfStage {
+  static constexpr int ST = 64;       // rows (or keys) per LDS stage
+  static constexpr int KS = DP + 8;   // LDS row stride in elements
+  static constexpr int CPR = DP / 8;  // 16-byte chunks per row
+};
+
+template <typename T>
+__device__ inline typename Mfma<T>::frag tr_frag(const T* tile_row0, int ks, int col) {
+  // 8 consecutive rows (k) at column `col` of this lane: two transposing reads of 4 rows
+  const i16x4 lo = lds_read_tr16(tile_row0 + col);
+  const i16x4 hi = lds_read_tr16(tile_row0 + 4 * ks + col);
+  const i16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(typename Mfma<T>::frag, both);
+}
+
+template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void bwd_dq_half_kernel(const BwdParams p) {
+  using M = Mfma<T>;
+  typedef typename M::frag F;
+  using S = HalfStage<T, DP>;
+  constexpr int KT = S::ST, KS = S::KS, CPR = S::CPR;
+  constexpr int NKK = DP / 16, NDT = DP / 32;
+  constexpr int NT = 64 * WAVES, ROWS_W = 32 * RT, BM = ROWS_W * WAVES;
+  static_assert((KT * CPR) % NT == 0, "staging must divide evenly");
+  constexpr int NCH = KT * CPR / NT;
+  __shared__ __attribute__((aligned(16))) T Ks[2][KT * KS];
+  __shared__ __attribute__((aligned(16))) T Vs[2][KT * KS];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int bh = blockIdx.y;
+  const int wg_row0 = blockIdx.x * BM;
+  const int wg_last = min(p.N, wg_row0 + BM) - 1;
+  const int row0 = wg_row0 + wave * ROWS_W;
+  const int64_t hoff = (int64_t)bh * p.N * p.D;
+  const T* Q = static_cast<const T*>(p.q) + hoff;
+  const T* K = static_cast<const T*>(p.k) + hoff;
+  const T* V = static_cast<const T*>(p.v) + hoff;
+  const T* dO = static_cast<const T*>(p.dout) + hoff;
+  const int bi = bh / p.H, hi = bh % p.H;
+  const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+  F qf[RT][NKK], gf[RT][NKK];
+  float lse[RT], dd[RT];
+  bool live[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = row0 + rt * 32 + c;
+    const bool ok = row < p.N;
+    const int rs = ok ? row : 0;
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      const int d0 = kk * 16 + g * 8;
+      qf[rt][kk] = load_frag<T>(Q + (int64_t)rs * p.D + d0, ok && d0 < p.D);
+      gf[rt][kk] = load_frag<T>(dO + (int64_t)rs * p.D + d0, ok && d0 < p.D);
+    }
+    lse[rt] = ok ? p.lse_row[(int64_t)bh * p.N + row] : 0.f;
+    dd[rt] = ok ? p.d_row[(int64_t)bh * p.N + row] : 0.f;
+    live[rt] = ok && lse[rt] > kNegInf;
+  }
+  const int k_end = p.causal ? wg_last + 1 : p.N;
+
+  Chunk16 kreg[NCH], vreg[NCH];
+  auto gload = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int ci = tid + i * NT;
+      const int r = ci / CPR, d0 = (ci % CPR) * 8;
+      if (t0 + r < k_end && d0 < p.D) {
+        const int64_t off = (int64_t)(t0 + r) * p.D + d0;
+        kreg[i] = *reinterpret_cast<const Chunk16*>(K + off);
+        vreg[i] = *reinterpret_cast<const Chunk16*>(V + off);
+      } else {
+        kreg[i] = Chunk16{};
+        vreg[i] = Chunk16{};
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int ci = tid + i * NT;
+      const int r = ci / CPR, d0 = (ci % CPR) * 8;
+      *reinterpret_cast<Chunk16*>(&Ks[buf][r * KS + d0]) = kreg[i];
+      *reinterpret_cast<Chunk16*>(&Vs[buf][r * KS + d0]) = vreg[i];
+    }
+  };
+
+  f32x16 acc[RT][NDT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[rt][dt] = f32x16{};
+
+  const int ntiles = (k_end + KT - 1) / KT;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    const int t0 = it * KT;
+    const bool has_next = it + 1 < ntiles;
+    if (has_next) gload(t0 + KT);
+    if (!p.causal || t0 <= row0 + ROWS_W - 1) {
+      const T* ks = Ks[buf];
+      const T* vs = Vs[buf];
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        F kf[NKK], vf[NKK];
+        const T* krow = ks + (sub * 32 + swap23(c)) * KS + g * 8;
+        const T* vrow = vs + (sub * 32 + swap23(c)) * KS + g * 8;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+          kf[kk] = *reinterpret_cast<const F*>(krow + kk * 16);
+          vf[kk] = *reinterpret_cast<const F*>(vrow + kk * 16);
+        }
+        f32x16 ds[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+          for (int kk = 0; kk < NKK; ++kk) {
+            s = M::mma(kf[kk], qf[rt][kk], s);
+            dp = M::mma(vf[kk], gf[rt][kk], dp);
+          }
+          const int my_row = row0 + rt * 32 + c;
+          const bool full = !HAS_BIAS && (t0 + KT <= k_end) && (!p.causal || t0 + KT - 1 <= row0 + rt * 32);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = t0 + sub * 32 + key_of_reg(r, g);
+            bool ok = live[rt];
+            if (!full) ok = ok && key < k_end && (!p.causal || key <= my_row);
+            float x = s[r] * p.scale_log2;
+            if constexpr (HAS_BIAS) x = ok ? fmaf(load_bias_b(p.bias, bi, hi, my_row, key), kLog2e, x) : x;
+            const float pr = ok ? fast_exp2(x - lse[rt]) : 0.f;
+            ds[rt][r] = pr * (dp[r] - dd[rt]);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          F ka[NDT];
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) ka[dt] = tr_frag<T>(ks + (sub * 32 + 16 * j + tr_row) * KS, KS, dt * 32 + tr_col);
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            F b;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) b[t] = static_cast<T>(ds[rt][j * 8 + t]);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) acc[rt][dt] = M::mma(ka[dt], b, acc[rt][dt]);
+          }
+        }
+      }
+    }
+    if (has_next) sstore(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int my_row = row0 + rt * 32 + c;
+    if (my_row >= p.N) continue;
+    T* out = static_cast<T*>(p.dq) + hoff + (int64_t)my_row * p.D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = dt * 32 + q4 * 8 + 4 * g;
+        if (d < p.D) {
+          typedef T t4 __attribute__((ext_vector_type(4)));
+          t4 v4 = {static_cast<T>(acc[rt][dt][4 * q4] * p.scale), static_cast<T>(acc[rt][dt][4 * q4 + 1] * p.scale),
+                   static_cast<T>(acc[rt][dt][4 * q4 + 2] * p.scale), static_cast<T>(acc[rt][dt][4 * q4 + 3] * p.scale)};
+          *reinterpret_cast<t4*>(out + d) = v4;
+        }
+      }
+  }
+}
+
+template <typename T, int DP, int KRT, int WAVES, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void bwd_dkdv_half_kernel(const BwdParams p) {
+  using M = Mfma<T>;
+  typedef typename M::frag F;
+  using S = HalfStage<T, DP>;
+  constexpr int RTS = S::ST, KS = S::KS, CPR = S::CPR;  // rows per stage
+  constexpr int NKK = DP / 16, NDT = DP / 32;
+  constexpr int NT = 64 * WAVES, KEYS_W = 32 * KRT, BN = KEYS_W * WAVES;
+  static_assert((RTS * CPR) % NT == 0, "staging must divide evenly");
+  constexpr int NCH = RTS * CPR / NT;
+  __shared__ __attribute__((aligned(16))) T Qs[2][RTS * KS];
+  __shared__ __attribute__((aligned(16))) T Gs[2][RTS * KS];
+  __shared__ __attribute__((aligned(16))) float lse_s[2][RTS];
+  __shared__ __attribute__((aligned(16))) float dd_s[2][RTS];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int bh = blockIdx.y;
+  const int wg_key0 = blockIdx.x * BN;
+  const int key0 = wg_key0 + wave * KEYS_W;
+  const int64_t hoff = (int64_t)bh * p.N * p.D;
+  const T* Q = static_cast<const T*>(p.q) + hoff;
+  const T* K = static_cast<const T*>(p.k) + hoff;
+  const T* V = static_cast<const T*>(p.v) + hoff;
+  const T* dO = static_cast<const T*>(p.dout) + hoff;
+  const int bi = bh / p.H, hi = bh % p.H;
+  const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+  F kf[KRT][NKK], vf[KRT][NKK];
+  bool key_ok[KRT];
+#pragma unroll
+  for (int kt = 0; kt < KRT; ++kt) {
+    const int key = key0 + kt * 32 + c;
+    key_ok[kt] = key < p.N;
+    const int ksafe = key_ok[kt] ? key : 0;
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      const int d0 = kk * 16 + g * 8;
+      kf[kt][kk] = load_frag<T>(K + (int64_t)ksafe * p.D + d0, key_ok[kt] && d0 < p.D);
+      vf[kt][kk] = load_frag<T>(V + (int64_t)ksafe * p.D + d0, key_ok[kt] && d0 < p.D);
+    }
+  }
+  f32x16 dk[KRT][NDT], dv[KRT][NDT];
+#pragma unroll
+  for (int kt = 0; kt < KRT; ++kt)
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      dk[kt][dt] = f32x16{};
+      dv[kt][dt] = f32x16{};
+    }
+
+  Chunk16 qreg[NCH], greg[NCH];
+  float lreg = 0.f, dreg = 0.f;
+  auto gload = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int ci = tid + i * NT;
+      const int r = ci / CPR, d0 = (ci % CPR) * 8;
+      if (t0 + r < p.N && d0 < p.D) {
+        const int64_t off = (int64_t)(t0 + r) * p.D + d0;
+        qreg[i] = *reinterpret_cast<const Chunk16*>(Q + off);
+        greg[i] = *reinterpret_cast<const Chunk16*>(dO + off);
+      } else {
+        qreg[i] = Chunk16{};
+        greg[i] = Chunk16{};
+      }
+    }
+    if (tid < RTS) {
+      const int ra = t0 + tid;
+      lreg = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : kNegInf;
+      dreg = ra < p.N ? p.d_row[(int64_t)bh * p.N + ra] : 0.f;
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int ci = tid + i * NT;
+      const int r = ci / CPR, d0 = (ci % CPR) * 8;
+      *reinterpret_cast<Chunk16*>(&Qs[buf][r * KS + d0]) = qreg[i];
+      *reinterpret_cast<Chunk16*>(&Gs[buf][r * KS + d0]) = greg[i];
+    }
+    if (tid < RTS) {
+      lse_s[buf][tid] = lreg;
+      dd_s[buf][tid] = dreg;
+    }
+  };
+
+  const int r_begin = p.causal ? (wg_key0 / RTS) * RTS : 0;
+  const int ntiles = (p.N - r_begin + RTS - 1) / RTS;
+  gload(r_begin);
+  sstore(0);
+  __syncthreads();
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    const int t0 = r_begin + it * RTS;
+    const bool has_next = it + 1 < ntiles;
+    if (has_next) gload(t0 + RTS);
+    if (!p.causal || t0 + RTS - 1 >= key0) {
+      const T* qs = Qs[buf];
+      const T* gs = Gs[buf];
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        F qa[NKK], ga[NKK];
+        const T* qrow = qs + (sub * 32 + swap23(c)) * KS + g * 8;
+        const T* grow = gs + (sub * 32 + swap23(c)) * KS + g * 8;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+          qa[kk] = *reinterpret_cast<const F*>(qrow + kk * 16);
+          ga[kk] = *reinterpret_cast<const F*>(grow + kk * 16);
+        }
+        // transposed Q^T / dO^T fragments for the dK / dV products, shared by the KRT key tiles
+        F gta[2][NDT], qta[2][NDT];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            gta[j][dt] = tr_frag<T>(gs + (sub * 32 + 16 * j + tr_row) * KS, KS, dt * 32 + tr_col);
+            qta[j][dt] = tr_frag<T>(qs + (sub * 32 + 16 * j + tr_row) * KS, KS, dt * 32 + tr_col);
+          }
+#pragma unroll
+        for (int kt = 0; kt < KRT; ++kt) {
+          f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+          for (int kk = 0; kk < NKK; ++kk) {
+            s = M::mma(qa[kk], kf[kt][kk], s);
+            dp = M::mma(ga[kk], vf[kt][kk], dp);
+          }
+          const int my_key = key0 + kt * 32 + c;
+          const bool full = !HAS_BIAS && (t0 + RTS <= p.N) && (!p.causal || t0 + sub * 32 >= key0 + kt * 32 + 31);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            // rows of registers 8j..8j+7: sub*32 + 16j + 8g + t (consecutive)
+            const float* lp = &lse_s[buf][sub * 32 + 16 * j + 8 * g];
+            const float* dq8 = &dd_s[buf][sub * 32 + 16 * j + 8 * g];
+            const f32x4 l0 = *reinterpret_cast<const f32x4*>(lp), l1 = *reinterpret_cast<const f32x4*>(lp + 4);
+            const f32x4 e0 = *reinterpret_cast<const f32x4*>(dq8), e1 = *reinterpret_cast<const f32x4*>(dq8 + 4);
+            F bp, bs;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+              const int r = 8 * j + t;
+              const float lr = t < 4 ? l0[t] : l1[t - 4];
+              const float dr = t < 4 ? e0[t] : e1[t - 4];
+              const int row = t0 + sub * 32 + key_of_reg(r, g);
+              bool ok = key_ok[kt] && lr > kNegInf;
+              if (!full) ok = ok && row < p.N && (!p.causal || row >= my_key);
+              float x = s[r] * p.scale_log2;
+              if constexpr (HAS_BIAS) x = ok ? fmaf(load_bias_b(p.bias, bi, hi, row, my_key), kLog2e, x) : x;
+              const float pr = ok ? fast_exp2(x - lr) : 0.f;
+              bp[t] = static_cast<T>(pr);
+              bs[t] = static_cast<T>(pr * (dp[r] - dr));
+            }
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+              dv[kt][dt] = M::mma(gta[j][dt], bp, dv[kt][dt]);
+              dk[kt][dt] = M::mma(qta[j][dt], bs, dk[kt][dt]);
+            }
+          }
+        }
+      }
+    }
+    if (has_next) sstore(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int kt = 0; kt < KRT; ++kt) {
+    const int my_key = key0 + kt * 32 + c;
+    if (my_key >= p.N) continue;
+    T* okp = static_cast<T*>(p.dk) + hoff + (int64_t)my_key * p.D;
+    T* ovp = static_cast<T*>(p.dv) + hoff + (int64_t)my_key * p.D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = dt * 32 + q4 * 8 + 4 * g;
+        if (d < p.D) {
+          typedef T t4 __attribute__((ext_vector_type(4)));
+          t4 k4 = {static_cast<T>(dk[kt][dt][4 * q4] * p.scale), static_cast<T>(dk[kt][dt][4 * q4 + 1] * p.scale),
+                   static_cast<T>(dk[kt][dt][4 * q4 + 2] * p.scale), static_cast<T>(dk[kt][dt][4 * q4 + 3] * p.scale)};
+          t4 v4 = {static_cast<T>(dv[kt][dt][4 * q4]), static_cast<T>(dv[kt][dt][4 * q4 + 1]),
+                   static_cast<T>(dv[kt][dt][4 * q4 + 2]), static_cast<T>(dv[kt][dt][4 * q4 + 3])};
+          *reinterpret_cast<t4*>(okp + d) = k4;
+          *reinterpret_cast<t4*>(ovp + d) = v4;
+        }
+      }
+  }
+}
+
 // ------------------------------------------------------------------ row stats
 template <typename T, int DP, int WAVES, bool HAS_BIAS>
 __global__ __launch_bounds__(64 * WAVES) void row_stats_kernel(const BwdParams p, float* row_m, float* row_z) {
@@ -423,21 +795,38 @@ static hipError_t pre_launch(const BwdParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+// fp16/bf16 kernels: 32 rows (dq) or 32 keys (dk/dv) per wave, 4 waves per
+// workgroup, register budget capped for 2 waves per SIMD (measured on MI355X at
+// B1 H8 N16K d64: dq 1.36 ms / dk-dv 1.68 ms versus 2.27 / 2.76 ms with 64-wide
+// wave tiles at 1 wave per SIMD).  fp32 keeps the 32-wide kernels above.
 template <typename T, int DP, bool B>
 static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
   constexpr int W = 4;
   hipError_t e = hipSuccess;
-  const dim3 grid((p.N + 32 * W - 1) / (32 * W), p.BH);
   if (stage < 0 || stage == 0) {
     if ((e = pre_launch<T>(p, st)) != hipSuccess) return e;
   }
-  if (stage < 0 || stage == 1) {
-    hipLaunchKernelGGL((bwd_dq_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
-  if (stage < 0 || stage == 2) {
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
-    e = hipGetLastError();
+  if constexpr (sizeof(T) == 2) {
+    constexpr int R = 1;  // one 32-wide tile per wave: 2 waves per SIMD beat wider tiles at 1
+    const dim3 grid((p.N + 32 * R * W - 1) / (32 * R * W), p.BH);
+    if (stage < 0 || stage == 1) {
+      hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, W, B>), grid, dim3(64 * W), 0, st, p);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    if (stage < 0 || stage == 2) {
+      hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, W, B>), grid, dim3(64 * W), 0, st, p);
+      e = hipGetLastError();
+    }
+  } else {
+    const dim3 grid((p.N + 32 * W - 1) / (32 * W), p.BH);
+    if (stage < 0 || stage == 1) {
+      hipLaunchKernelGGL((bwd_dq_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    if (stage < 0 || stage == 2) {
+      hipLaunchKernelGGL((bwd_dkdv_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
+      e = hipGetLastError();
+    }
   }
   return e;
 }

@@ -52,7 +52,7 @@ struct FwdCfg {
 
 int phase1_key_tile(int dtype, int dp) {
   if (dtype == ELSA_F32) return dp >= 64 ? 32 : 64;
-  return dp == 128 ? 32 : 64;
+  return 64;
 }
 
 __device__ inline float load_bias(const BiasView& b, int bi, int hi, int row, int key) {
@@ -286,6 +286,258 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
     }
 }
 
+// ------------------------------------------------------------------ Phase 1, fp16 / bf16
+// Each wave owns RT 32-row tiles (RT = 2 for head dims <= 64) so one K/V
+// fragment read from LDS feeds RT MFMAs.  K and V are staged row-major with
+// 16-byte copies; the V^T operand of O^T += V^T P^T is read with the transposing
+// LDS load.  The running max is lazy: it is raised only when a 64-key stage
+// exceeds it by more than kLazyTau (p stays <= 2^kLazyTau, exact in fp16/bf16 and
+// fp32), and the summary is renormalised to the exact row maximum at the end.
+// The row sum accumulates the same 16-bit p values that feed the MFMA.
+constexpr float kLazyTau = 8.0f;
+
+template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void phase1_half_kernel(const Phase1Params p) {
+  using M = Mfma<T>;
+  typedef typename M::frag F;
+  constexpr int KT = 64;          // keys per LDS stage
+  constexpr int NSUB = KT / 32;   // 32-key sub-tiles per stage
+  constexpr int NKK = DP / 16;    // MFMAs over the head dim
+  constexpr int NDT = DP / 32;    // 32-wide head-dim tiles of O^T
+  constexpr int KS = DP + 8;      // LDS row stride (elements) of the K and V tiles
+  constexpr int NT = 64 * WAVES;
+  constexpr int ROWS_W = 32 * RT;
+  constexpr int BM = ROWS_W * WAVES;
+  constexpr int CPR = DP / 8;     // 16-byte chunks per key row
+  static_assert((KT * CPR) % NT == 0, "staging must divide evenly");
+  constexpr int NCH = KT * CPR / NT;
+
+  __shared__ __attribute__((aligned(16))) T Ks[2][KT * KS];
+  __shared__ __attribute__((aligned(16))) T Vs[2][KT * KS];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int bh = blockIdx.y, kb = blockIdx.z;
+  const int q_end = p.q_start + p.q_len;
+  const int wg_row0 = p.q_start + blockIdx.x * BM;
+  const int wg_last = min(q_end, wg_row0 + BM) - 1;
+  const int k_begin = kb * p.part_len;
+  int k_end = min(p.N, k_begin + p.part_len);
+  if (p.causal) k_end = min(k_end, wg_last + 1);
+  if (k_begin >= k_end) return;  // every row of this workgroup sees the identity here
+
+  const int row0 = wg_row0 + wave * ROWS_W;
+  const int64_t hoff = (int64_t)bh * p.N * p.D;
+  const T* __restrict__ Q = static_cast<const T*>(p.q) + hoff;
+  const T* __restrict__ K = static_cast<const T*>(p.k) + hoff;
+  const T* __restrict__ V = static_cast<const T*>(p.v) + hoff;
+  const int bi = bh / p.H, hi = bh - (bh / p.H) * p.H;
+
+  F qf[RT][NKK];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = row0 + rt * 32 + c;
+    const bool ok = row < q_end;
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      const int d0 = kk * 16 + g * 8;
+      qf[rt][kk] = load_frag<T>(Q + (int64_t)(ok ? row : 0) * p.D + d0, ok && d0 < p.D);
+    }
+  }
+
+  // transposing-read coordinates of this lane (see lds_read_tr16)
+  const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+  Chunk16 kreg[NCH], vreg[NCH];
+  auto gload = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int ci = tid + i * NT;
+      const int key = ci / CPR, d0 = (ci % CPR) * 8;
+      const int ka = t0 + key;
+      if (ka < k_end && d0 < p.D) {
+        const int64_t off = (int64_t)ka * p.D + d0;
+        kreg[i] = *reinterpret_cast<const Chunk16*>(K + off);
+        vreg[i] = *reinterpret_cast<const Chunk16*>(V + off);
+      } else {
+        kreg[i] = Chunk16{};
+        vreg[i] = Chunk16{};
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int ci = tid + i * NT;
+      const int key = ci / CPR, d0 = (ci % CPR) * 8;
+      *reinterpret_cast<Chunk16*>(&Ks[buf][key * KS + d0]) = kreg[i];
+      *reinterpret_cast<Chunk16*>(&Vs[buf][key * KS + d0]) = vreg[i];
+    }
+  };
+
+  f32x16 oacc[RT][NDT];
+  float m_run[RT], m_true[RT], z_lane[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    m_run[rt] = kNegInf;
+    m_true[rt] = kNegInf;
+    z_lane[rt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) oacc[rt][dt] = f32x16{};
+  }
+  const float cs = p.scale_log2;
+  const int ntiles = (k_end - k_begin + KT - 1) / KT;
+
+  gload(k_begin);
+  sstore(0);
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    const int t0 = k_begin + it * KT;
+    const bool has_next = it + 1 < ntiles;
+    if (has_next) gload(t0 + KT);
+    // a causal wave whose rows all precede this stage has nothing to add
+    const bool active = !p.causal || t0 <= row0 + ROWS_W - 1;
+    if (active) {
+      const T* ks = Ks[buf];
+      const T* vs = Vs[buf];
+      f32x16 s[RT][NSUB];
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub) {
+        const T* krow = ks + (sub * 32 + swap23(c)) * KS + g * 8;
+        F kf[NKK];
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) kf[kk] = *reinterpret_cast<const F*>(krow + kk * 16);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          s[rt][sub] = f32x16{};
+#pragma unroll
+          for (int kk = 0; kk < NKK; ++kk) s[rt][sub] = M::mma(kf[kk], qf[rt][kk], s[rt][sub]);
+        }
+      }
+
+      float m_tile[RT];
+      bool raise = false;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const int my_row = row0 + rt * 32 + c;
+        float mx = kNegInf;
+        if constexpr (HAS_BIAS) {
+          const bool row_ok = my_row < q_end;
+#pragma unroll
+          for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = t0 + sub * 32 + key_of_reg(r, g);
+              const bool ok = row_ok && key < k_end && (!p.causal || key <= my_row);
+              const float x =
+                  ok ? fmaf(s[rt][sub][r], cs, load_bias(p.bias, bi, hi, my_row, key) * p.bias_log2) : kNegInf;
+              s[rt][sub][r] = x;
+              mx = fmaxf(mx, x);
+            }
+        } else {
+          const bool need_mask = (t0 + KT > k_end) || (p.causal && (t0 + KT - 1 > row0 + rt * 32));
+          if (need_mask) {
+#pragma unroll
+            for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int key = t0 + sub * 32 + key_of_reg(r, g);
+                if (!(key < k_end && (!p.causal || key <= my_row))) s[rt][sub][r] = kNegInf;
+              }
+          }
+#pragma unroll
+          for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[rt][sub][r], s[rt][sub][r + 1]));
+        }
+        mx = wave_max_pair(mx);
+        m_tile[rt] = HAS_BIAS ? mx : mx * cs;
+        m_true[rt] = fmaxf(m_true[rt], m_tile[rt]);
+        raise |= m_tile[rt] > m_run[rt] + kLazyTau;
+      }
+      if (__any(raise)) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const float m_new = fmaxf(m_run[rt], m_tile[rt]);
+          const float alpha = (m_run[rt] == kNegInf) ? 0.f : fast_exp2(m_run[rt] - m_new);
+          z_lane[rt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[rt][dt][r] *= alpha;
+          m_run[rt] = m_new;
+        }
+      }
+
+      // p = exp2(score - m_run); O^T += V^T P^T with V^T fragments shared by the RT row tiles
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const float nm = (m_run[rt] == kNegInf) ? 0.f : -m_run[rt];
+        float zs = 0.f;
+#pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float pr = HAS_BIAS ? fast_exp2(s[rt][sub][r] + nm) : fast_exp2(fmaf(s[rt][sub][r], cs, nm));
+            s[rt][sub][r] = pr;
+            zs += pr;
+          }
+        z_lane[rt] += zs;
+      }
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          F va[NDT];
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const T* base = vs + (sub * 32 + 16 * j + tr_row) * KS + dt * 32 + tr_col;
+            const i16x4 lo = lds_read_tr16(base);
+            const i16x4 hi4 = lds_read_tr16(base + 4 * KS);
+            const i16x8 both = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+            va[dt] = __builtin_bit_cast(F, both);
+          }
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            F b;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) b[t] = static_cast<T>(s[rt][sub][j * 8 + t]);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) oacc[rt][dt] = M::mma(va[dt], b, oacc[rt][dt]);
+          }
+        }
+    }
+    if (has_next) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const float z_raw = wave_sum_pair(z_lane[rt]);
+    const int my_row = row0 + rt * 32 + c;
+    if (my_row >= q_end) continue;
+    // renormalise to the exact row maximum (m_run <= m_true <= m_run + kLazyTau)
+    const float f = (m_true[rt] == kNegInf) ? 1.f : fast_exp2(m_run[rt] - m_true[rt]);
+    const int64_t ridx = ((int64_t)kb * p.BH + bh) * p.rows_pad + (my_row - p.q_start);
+    if (g == 0) {
+      p.m_buf[ridx] = m_true[rt];
+      p.z_buf[ridx] = z_raw * f;
+    }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = dt * 32 + q4 * 8 + 4 * g;
+        if (d < p.D)
+          store4(p.s_buf, ridx * p.D + d, p.s_dtype, oacc[rt][dt][4 * q4] * f, oacc[rt][dt][4 * q4 + 1] * f,
+                 oacc[rt][dt][4 * q4 + 2] * f, oacc[rt][dt][4 * q4 + 3] * f);
+      }
+  }
+}
+
 // ------------------------------------------------------------------ Phase 2
 template <typename ST>
 __device__ inline void load8(const void* base, int64_t off, float (&dst)[8]) {
@@ -385,26 +637,54 @@ static hipError_t launch1(const Phase1Params& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <typename T, int DP>
-static hipError_t launch1_wb(const Phase1Params& p, int waves, hipStream_t st) {
-  const bool b = p.bias.ptr != nullptr;
-  if (waves == 2) return b ? launch1<T, DP, 2, true>(p, st) : launch1<T, DP, 2, false>(p, st);
-  return b ? launch1<T, DP, 4, true>(p, st) : launch1<T, DP, 4, false>(p, st);
+template <typename T, int DP, int RT, int W, bool B>
+static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
+  constexpr int BM = 32 * RT * W;
+  const dim3 grid((p.q_len + BM - 1) / BM, p.BH, p.P);
+  hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, B>), grid, dim3(64 * W), 0, st, p);
+  return hipGetLastError();
 }
 
-template <typename T>
-static hipError_t launch1_d(const Phase1Params& p, int waves, hipStream_t st) {
-  switch (pad_head_dim(p.D)) {
-    case 32: return launch1_wb<T, 32>(p, waves, st);
-    case 64: return launch1_wb<T, 64>(p, waves, st);
-    default: return launch1_wb<T, 128>(p, waves, st);
+// fp16/bf16: 64 rows per wave for head dims <= 64 (32 for 128); 1 (or 2) waves for
+// sequences of at most 64 rows, 4 waves otherwise.  fp32: 32 rows per wave.
+int phase1_rows_per_wave(int dtype, int dp) { return (dtype != ELSA_F32 && dp <= 64) ? 64 : 32; }
+
+template <typename T, int DP>
+static hipError_t launch1h_wb(const Phase1Params& p, int waves, hipStream_t st) {
+  const bool b = p.bias.ptr != nullptr;
+  if constexpr (DP <= 64) {
+    if (waves == 1) return b ? launch1h<T, DP, 2, 1, true>(p, st) : launch1h<T, DP, 2, 1, false>(p, st);
+    return b ? launch1h<T, DP, 2, 4, true>(p, st) : launch1h<T, DP, 2, 4, false>(p, st);
+  } else {
+    if (waves == 2) return b ? launch1h<T, DP, 1, 2, true>(p, st) : launch1h<T, DP, 1, 2, false>(p, st);
+    return b ? launch1h<T, DP, 1, 4, true>(p, st) : launch1h<T, DP, 1, 4, false>(p, st);
   }
 }
 
+template <typename T>
+static hipError_t launch1h_d(const Phase1Params& p, int waves, hipStream_t st) {
+  switch (pad_head_dim(p.D)) {
+    case 32: return launch1h_wb<T, 32>(p, waves, st);
+    case 64: return launch1h_wb<T, 64>(p, waves, st);
+    default: return launch1h_wb<T, 128>(p, waves, st);
+  }
+}
+
+template <int DP>
+static hipError_t launch1_f32_wb(const Phase1Params& p, int waves, hipStream_t st) {
+  const bool b = p.bias.ptr != nullptr;
+  if (waves == 2) return b ? launch1<float, DP, 2, true>(p, st) : launch1<float, DP, 2, false>(p, st);
+  return b ? launch1<float, DP, 4, true>(p, st) : launch1<float, DP, 4, false>(p, st);
+}
+
 hipError_t launch_phase1(const Phase1Params& p, int dtype, int waves, hipStream_t st) {
-  if (dtype == ELSA_F16) return launch1_d<f16>(p, waves, st);
-  if (dtype == ELSA_BF16) return launch1_d<bf16>(p, waves, st);
-  return launch1_d<float>(p, waves, st);
+  if (dtype == ELSA_F16) return launch1h_d<f16>(p, waves, st);
+  if (dtype == ELSA_BF16) return launch1h_d<bf16>(p, waves, st);
+  switch (pad_head_dim(p.D)) {
+    case 32: return launch1_f32_wb<32>(p, waves, st);
+    case 64: return launch1_f32_wb<64>(p, waves, st);
+    default: return launch1_f32_wb<128>(p, waves, st);
+  }
 }
 
 template <typename ST, typename TO>

@@ -8,8 +8,6 @@
 
 namespace elsa {
 
-// Phase-1 workgroup shape: 32 query rows per wave (one 32-row MFMA tile).
-constexpr int kRowsPerWave = 32;
 
 struct BiasView {
   const void* ptr;
@@ -59,6 +57,7 @@ struct Phase2Params {
 hipError_t launch_phase1(const Phase1Params& p, int dtype, int waves, hipStream_t stream);
 hipError_t launch_phase2(const Phase2Params& p, hipStream_t stream);
 int phase1_key_tile(int dtype, int head_dim_padded);
+int phase1_rows_per_wave(int dtype, int head_dim_padded);
 int pad_head_dim(int d);
 
 struct BwdParams {

@@ -26,6 +26,10 @@ typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -109,6 +113,25 @@ __device__ inline typename Mfma<T>::frag pack_frag(const f32x16& v) {
 struct alignas(16) Chunk16 {
   uint32_t w[4];
 };
+
+// acc + a + b with an fp32 accumulator (v_dot2_f32_f16 / v_dot2_f32_bf16 against (1, 1)).
+__device__ inline float sum2(f16 a, f16 b, float acc) {
+  const f16x2 v = {a, b}, one = {(f16)1.0f, (f16)1.0f};
+  return __builtin_amdgcn_fdot2(v, one, acc, false);
+}
+__device__ inline float sum2(bf16 a, bf16 b, float acc) {
+  const bf16x2 v = {a, b}, one = {(bf16)1.0f, (bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(v, one, acc, false);
+}
+
+// Transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane group, source
+// lane s = 4t + a reads 4 16-bit elements at its own address; result lane
+// i = 4a' + b' receives element b' of source lanes a' + 4t, t = 0..3.  Pointing
+// source lane 4t + a at &M[k0 + t][d0 + 4a] of a row-major tile therefore gives
+// lane i the column segment M[k0 .. k0+3][d0 + i].
+__device__ inline i16x4 lds_read_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)p);
+}
 
 __device__ inline float wave_max_pair(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 __device__ inline float wave_sum_pair(float x) { return x + __shfl_xor(x, 32); }

@@ -62,7 +62,7 @@ def test_plan_north_star_routing():
     rc, p = _plan(_args())
     assert rc == 0
     assert p.partitions >= 2 and p.partitions * p.partition_len >= 16384
-    assert p.q_chunk == 16384 and p.block_m == 128 and p.key_tile == 64
+    assert p.q_chunk == 16384 and p.block_m == 256 and p.key_tile == 64
     rows = p.partitions * 8 * 16384
     assert p.workspace_bytes >= rows * (8 + 64 * 2)
 

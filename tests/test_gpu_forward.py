@@ -66,7 +66,7 @@ def test_forward_matches_oracle_and_closed_form(case):
     qf, kf, vf = (np.asarray(x, np.float32) for x in (q, k, v))
     eo, em, ez = O.exact_forward(qf, kf, vf, is_causal=causal)
     ro, _, _ = O.forward(q, k, v, is_causal=causal, part_len=bn, dtype=dt, mode="ref")
-    describe(str(assert_parity(host(out), eo, ro, FWD_TOL[dt], "out")))
+    describe(str(assert_parity(host(out), eo, ro, FWD_TOL[dt], "out", dt)))
     m = host(row_m)
     assert np.array_equal(np.isneginf(m), np.isneginf(em))
     fin = np.isfinite(em)
@@ -84,7 +84,7 @@ def test_forward_bias(dt, bias_shape):
     out = elsa_amd.twopass_attention(dev(q, dt), dev(k, dt), dev(v, dt), bias=dev(bias, "fp32"))
     eo, _, _ = O.exact_forward(np.float32(q), np.float32(k), np.float32(v), bias=bias)
     ro, _, _ = O.forward(q, k, v, bias=bias, dtype=dt, mode="ref")
-    assert_parity(host(out), eo, ro, FWD_TOL[dt], "out")
+    assert_parity(host(out), eo, ro, FWD_TOL[dt], "out", dt)
 
 
 @pytest.mark.parametrize("dt", ["fp32", "fp16"])
@@ -99,7 +99,7 @@ def test_forward_swin_window_bias_and_shift_mask(dt):
     out = elsa_amd.twopass_attention(dev(q, dt), dev(k, dt), dev(v, dt), bias=dev(bias, "fp32"))
     eo, _, _ = O.exact_forward(np.float32(q), np.float32(k), np.float32(v), bias=bias)
     ro, _, _ = O.forward(q, k, v, bias=bias, dtype=dt, mode="ref")
-    describe(str(assert_parity(host(out), eo, ro, FWD_TOL[dt], "out")))
+    describe(str(assert_parity(host(out), eo, ro, FWD_TOL[dt], "out", dt)))
 
 
 def test_fully_masked_rows_return_zero_and_identity_state():
