@@ -47,6 +47,8 @@ def _args():
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--cpu-rows", type=int, default=512, help="query rows of the CPU-baseline sample")
     ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "traffic_north_star.json"))
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="after timing, run one device-to-device copy of this many MiB (HBM-counter calibration)")
     return ap.parse_args()
 
 
@@ -229,6 +231,13 @@ def main() -> int:
         "kernels": kernels,
         "roofline": roofline,
     }
+    if args.copy_mib > 0:
+        src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        result["copy_calibration_mib"] = args.copy_mib
     if args.cpu_baseline:
         result["cpu_baseline"] = _cpu_baseline(args, B, H, N, D, causal)
     print(json.dumps(result), flush=True)

@@ -26,6 +26,9 @@ HIP_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # scores and p are never NaN by construction (masking uses -inf), so min/max
+    # need no NaN-quieting canonicalisation of their inputs
+    "-fno-honor-nans",
     "-Wno-unused-result",
 ]
 

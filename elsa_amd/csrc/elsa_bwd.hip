@@ -98,7 +98,10 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdParams p) {
     for (int t = 0; t < 16 / (int)sizeof(T); ++t) acc = fmaf(static_cast<float>(ea[t]), static_cast<float>(eb[t]), acc);
   }
   p.d_row[i] = acc;
-  p.lse_row[i] = p.row_m[i] + __log2f(fmaxf(p.row_z[i], 1.0e-30f));
+  // LSE2 = m + log2(max(z, 1e-30)) (attention_bwd.py:224); a row with no valid key
+  // (z == 0) stores +inf instead of -inf so that p = exp2(s - LSE2) is 0 without a test.
+  const float z = p.row_z[i];
+  p.lse_row[i] = z > 0.f ? p.row_m[i] + __log2f(fmaxf(z, 1.0e-30f)) : __builtin_huge_valf();
 }
 
 // ------------------------------------------------------------------ dq
@@ -113,7 +116,8 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) T Kt[DP * C::TS];
   __shared__ __attribute__((aligned(16))) T Vt[C::HALF ? 1 : DP * C::TS];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
+            g = lane >> 5;
   const int bh = blockIdx.y;
   const int wg_row0 = blockIdx.x * BM;
   const int wg_last = min(p.N, wg_row0 + BM) - 1;
@@ -203,7 +207,8 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dkdv_kernel(const BwdParams p)
   __shared__ __attribute__((aligned(16))) T Gt[DP * C::TS];
   __shared__ float lse_s[C::TT], dd_s[C::TT];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
+            g = lane >> 5;
   const int bh = blockIdx.y;
   const int wg_key0 = blockIdx.x * BN;
   const int key0 = wg_key0 + wave * 32;
@@ -333,7 +338,8 @@ void bwd_dq_half_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) T Ks[2][KT * KS];
   __shared__ __attribute__((aligned(16))) T Vs[2][KT * KS];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
+            g = lane >> 5;
   const int bh = blockIdx.y;
   const int wg_row0 = blockIdx.x * BM;
   const int wg_last = min(p.N, wg_row0 + BM) - 1;
@@ -361,9 +367,9 @@ void bwd_dq_half_kernel(const BwdParams p) {
       qf[rt][kk] = load_frag<T>(Q + (int64_t)rs * p.D + d0, ok && d0 < p.D);
       gf[rt][kk] = load_frag<T>(dO + (int64_t)rs * p.D + d0, ok && d0 < p.D);
     }
-    lse[rt] = ok ? p.lse_row[(int64_t)bh * p.N + row] : 0.f;
+    lse[rt] = ok ? p.lse_row[(int64_t)bh * p.N + row] : __builtin_huge_valf();
     dd[rt] = ok ? p.d_row[(int64_t)bh * p.N + row] : 0.f;
-    live[rt] = ok && lse[rt] > kNegInf;
+    live[rt] = ok && lse[rt] < __builtin_huge_valf();
   }
   const int k_end = p.causal ? wg_last + 1 : p.N;
 
@@ -431,16 +437,30 @@ void bwd_dq_half_kernel(const BwdParams p) {
             dp = M::mma(vf[kk], gf[rt][kk], dp);
           }
           const int my_row = row0 + rt * 32 + c;
-          const bool full = !HAS_BIAS && (t0 + KT <= k_end) && (!p.causal || t0 + KT - 1 <= row0 + rt * 32);
+          const bool full = (t0 + KT <= k_end) && (!p.causal || t0 + KT - 1 <= row0 + rt * 32);
+          const float nl = -lse[rt];
+          if constexpr (HAS_BIAS) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = t0 + sub * 32 + key_of_reg(r, g);
-            bool ok = live[rt];
-            if (!full) ok = ok && key < k_end && (!p.causal || key <= my_row);
-            float x = s[r] * p.scale_log2;
-            if constexpr (HAS_BIAS) x = ok ? fmaf(load_bias_b(p.bias, bi, hi, my_row, key), kLog2e, x) : x;
-            const float pr = ok ? fast_exp2(x - lse[rt]) : 0.f;
-            ds[rt][r] = pr * (dp[r] - dd[rt]);
+            for (int r = 0; r < 16; ++r) {
+              const int key = t0 + sub * 32 + key_of_reg(r, g);
+              const bool ok = live[rt] && key < k_end && (!p.causal || key <= my_row);
+              const float x = fmaf(s[r], p.scale_log2, nl);
+              const float pr = ok ? fast_exp2(fmaf(load_bias_b(p.bias, bi, hi, my_row, key), kLog2e, x)) : 0.f;
+              ds[rt][r] = pr * (dp[r] - dd[rt]);
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ds[rt][r] = fast_exp2(fmaf(s[r], p.scale_log2, nl));
+            if (!full) {
+              asm volatile("");  // keep this a branch: boundary tiles only
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int key = t0 + sub * 32 + key_of_reg(r, g);
+                if (!(key < k_end && (!p.causal || key <= my_row))) ds[rt][r] = 0.f;
+              }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ds[rt][r] *= dp[r] - dd[rt];
           }
         }
 #pragma unroll
@@ -498,7 +518,8 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) float lse_s[2][RTS];
   __shared__ __attribute__((aligned(16))) float dd_s[2][RTS];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
+            g = lane >> 5;
   const int bh = blockIdx.y;
   const int wg_key0 = blockIdx.x * BN;
   const int key0 = wg_key0 + wave * KEYS_W;
@@ -550,9 +571,9 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
         greg[i] = Chunk16{};
       }
     }
-    if (tid < RTS) {
+    if (tid < RTS) {  // rows past N: LSE2 = +inf makes their p exactly 0
       const int ra = t0 + tid;
-      lreg = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : kNegInf;
+      lreg = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : __builtin_huge_valf();
       dreg = ra < p.N ? p.d_row[(int64_t)bh * p.N + ra] : 0.f;
     }
   };
@@ -611,7 +632,7 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
             dp = M::mma(ga[kk], vf[kt][kk], dp);
           }
           const int my_key = key0 + kt * 32 + c;
-          const bool full = !HAS_BIAS && (t0 + RTS <= p.N) && (!p.causal || t0 + sub * 32 >= key0 + kt * 32 + 31);
+          const bool full = (key0 + kt * 32 + 31 < p.N) && (t0 + RTS <= p.N) && (!p.causal || t0 + sub * 32 >= key0 + kt * 32 + 31);
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             // rows of registers 8j..8j+7: sub*32 + 16j + 8g + t (consecutive)
@@ -619,20 +640,33 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
             const float* dq8 = &dd_s[buf][sub * 32 + 16 * j + 8 * g];
             const f32x4 l0 = *reinterpret_cast<const f32x4*>(lp), l1 = *reinterpret_cast<const f32x4*>(lp + 4);
             const f32x4 e0 = *reinterpret_cast<const f32x4*>(dq8), e1 = *reinterpret_cast<const f32x4*>(dq8 + 4);
+            float pr[8];
+            if constexpr (HAS_BIAS) {
+#pragma unroll
+              for (int t = 0; t < 8; ++t) {
+                const int row = t0 + sub * 32 + key_of_reg(8 * j + t, g);
+                const float lr = t < 4 ? l0[t] : l1[t - 4];
+                const bool ok = key_ok[kt] && row < p.N && (!p.causal || row >= my_key);
+                const float x = fmaf(s[8 * j + t], p.scale_log2, -lr);
+                pr[t] = ok ? fast_exp2(fmaf(load_bias_b(p.bias, bi, hi, row, my_key), kLog2e, x)) : 0.f;
+              }
+            } else {
+#pragma unroll
+              for (int t = 0; t < 8; ++t) pr[t] = fast_exp2(fmaf(s[8 * j + t], p.scale_log2, t < 4 ? -l0[t] : -l1[t - 4]));
+              if (!full) {
+                asm volatile("");  // keep this a branch: boundary tiles only
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                  const int row = t0 + sub * 32 + key_of_reg(8 * j + t, g);
+                  if (!(key_ok[kt] && row < p.N && (!p.causal || row >= my_key))) pr[t] = 0.f;
+                }
+              }
+            }
             F bp, bs;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-              const int r = 8 * j + t;
-              const float lr = t < 4 ? l0[t] : l1[t - 4];
-              const float dr = t < 4 ? e0[t] : e1[t - 4];
-              const int row = t0 + sub * 32 + key_of_reg(r, g);
-              bool ok = key_ok[kt] && lr > kNegInf;
-              if (!full) ok = ok && row < p.N && (!p.causal || row >= my_key);
-              float x = s[r] * p.scale_log2;
-              if constexpr (HAS_BIAS) x = ok ? fmaf(load_bias_b(p.bias, bi, hi, row, my_key), kLog2e, x) : x;
-              const float pr = ok ? fast_exp2(x - lr) : 0.f;
-              bp[t] = static_cast<T>(pr);
-              bs[t] = static_cast<T>(pr * (dp[r] - dr));
+              bp[t] = static_cast<T>(pr[t]);
+              bs[t] = static_cast<T>(pr[t] * (dp[8 * j + t] - (t < 4 ? e0[t] : e1[t - 4])));
             }
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
@@ -679,7 +713,8 @@ __global__ __launch_bounds__(64 * WAVES) void row_stats_kernel(const BwdParams p
   constexpr int NT = 64 * WAVES, BM = 32 * WAVES;
   __shared__ __attribute__((aligned(16))) T Ks[C::HALF ? C::TT * C::RS : 1];
   __shared__ __attribute__((aligned(16))) T Kt[C::HALF ? 1 : DP * C::TS];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
+            g = lane >> 5;
   const int bh = blockIdx.y;
   const int wg_row0 = blockIdx.x * BM;
   const int wg_last = min(p.N, wg_row0 + BM) - 1;

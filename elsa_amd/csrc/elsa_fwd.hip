@@ -92,7 +92,7 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
   __shared__ __attribute__((aligned(16))) T Vt[C::NBUF][DP * C::VS];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31, g = lane >> 5;
   const int bh = blockIdx.y, kb = blockIdx.z;
   const int q_end = p.q_start + p.q_len;
   const int wg_row0 = p.q_start + blockIdx.x * BM;
@@ -316,7 +316,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   __shared__ __attribute__((aligned(16))) T Vs[2][KT * KS];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31, g = lane >> 5;
   const int bh = blockIdx.y, kb = blockIdx.z;
   const int q_end = p.q_start + p.q_len;
   const int wg_row0 = p.q_start + blockIdx.x * BM;

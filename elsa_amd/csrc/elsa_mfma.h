@@ -133,7 +133,15 @@ __device__ inline i16x4 lds_read_tr16(const void* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)p);
 }
 
-__device__ inline float wave_max_pair(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
-__device__ inline float wave_sum_pair(float x) { return x + __shfl_xor(x, 32); }
+// Combine the two 32-lane halves of a wave (lanes l and l ^ 32) with
+// v_permlane32_swap: both results hold one value of each half.
+__device__ inline float wave_max_pair(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float wave_sum_pair(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 }  // namespace elsa
