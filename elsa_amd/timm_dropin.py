@@ -1,0 +1,193 @@
+"""timm drop-in (inference): swap ViT / Swin v1 attention modules for two-pass ELSA.
+
+Mirrors the reference's timm_dropin.py (``PatchReport`` :13-20, ``ElsaTimmVitAttention``
+:23-59, ``ElsaTimmSwinWindowAttention`` :62-150, duck-typing predicates :153-172,
+``patch_timm_attention`` :175-194): same class names, patched attributes, kwargs and
+errors.  The attention call goes to ``twopass_attention`` (HIP two-pass kernels);
+Swin windows pass the relative-position bias plus the shifted-window mask as one
+broadcast bias.  ``set_window_size`` uses this package's own index/resize helpers
+(elsa_amd.vision_models) instead of timm's.
+"""
+from __future__ import annotations
+
+import copy
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from .attention import twopass_attention
+from .vision_models import relative_position_index, resize_rel_pos_bias_table
+
+
+@dataclass(frozen=True)
+class PatchReport:
+    vit_attention: int = 0
+    swin_window_attention: int = 0
+
+    @property
+    def total(self) -> int:
+        return self.vit_attention + self.swin_window_attention
+
+
+def _vit_state(module: nn.Module, source: nn.Module, elsa_kwargs: Optional[dict]) -> None:
+    module.num_heads = int(source.num_heads)
+    module.head_dim = int(source.head_dim)
+    module.attn_dim = int(getattr(source, "attn_dim", module.num_heads * module.head_dim))
+    module.qkv = copy.deepcopy(source.qkv)
+    module.q_norm = copy.deepcopy(source.q_norm)
+    module.k_norm = copy.deepcopy(source.k_norm)
+    module.norm = copy.deepcopy(source.norm) if hasattr(source, "norm") else nn.Identity()
+    module.proj = copy.deepcopy(source.proj)
+    module.proj_drop = copy.deepcopy(source.proj_drop)
+    module.elsa_kwargs = dict(elsa_kwargs or {})
+
+
+def _vit_qkv(module: nn.Module, x: torch.Tensor):
+    batch, seq_len, _ = x.shape
+    # one contiguous [3, B, H, N, D] tensor so the unbound q/k/v need no further copies
+    qkv = module.qkv(x).reshape(batch, seq_len, 3, module.num_heads, module.head_dim).permute(2, 0, 3, 1, 4)
+    q, k, v = qkv.contiguous().unbind(0)
+    return module.q_norm(q), module.k_norm(k), v
+
+
+def _vit_out(module: nn.Module, y: torch.Tensor, batch: int, seq_len: int) -> torch.Tensor:
+    y = y.transpose(1, 2).reshape(batch, seq_len, module.attn_dim)
+    return module.proj_drop(module.proj(module.norm(y)))
+
+
+class ElsaTimmVitAttention(nn.Module):
+    def __init__(self, source: nn.Module, *, elsa_kwargs: Optional[dict] = None) -> None:
+        super().__init__()
+        _vit_state(self, source, elsa_kwargs)
+
+    def forward(self, x: torch.Tensor, attn_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if attn_mask is not None:
+            raise ValueError("ELSA ViT drop-in currently supports unmasked attention only")
+        q, k, v = _vit_qkv(self, x)
+        y = twopass_attention(q, k, v, **self.elsa_kwargs)
+        return _vit_out(self, y, x.shape[0], x.shape[1])
+
+
+def _swin_state(module: nn.Module, source: nn.Module, elsa_kwargs: Optional[dict]) -> None:
+    module.dim = int(source.dim)
+    module.window_size = tuple(int(x) for x in source.window_size)
+    module.window_area = int(source.window_area)
+    module.num_heads = int(source.num_heads)
+    module.qkv = copy.deepcopy(source.qkv)
+    module.attn_drop = copy.deepcopy(source.attn_drop)
+    module.proj = copy.deepcopy(source.proj)
+    module.proj_drop = copy.deepcopy(source.proj_drop)
+    module.softmax = copy.deepcopy(source.softmax)
+    module.scale = float(source.scale)
+    module.head_dim = int(module.qkv.out_features // (3 * module.num_heads))
+    module.attn_dim = module.head_dim * module.num_heads
+    module.relative_position_bias_table = nn.Parameter(source.relative_position_bias_table.detach().clone())
+    module.register_buffer("relative_position_index", source.relative_position_index.detach().clone(),
+                           persistent=False)
+    module.elsa_kwargs = dict(elsa_kwargs or {})
+
+
+class _SwinWindowCommon(nn.Module):
+    """Shared pieces of the Swin v1 window-attention drop-ins (reference timm_dropin.py:85-144)."""
+
+    def _get_rel_pos_bias(self) -> torch.Tensor:
+        bias = self.relative_position_bias_table[self.relative_position_index.view(-1)].view(
+            self.window_area, self.window_area, self.num_heads)
+        return bias.permute(2, 0, 1).contiguous().unsqueeze(0)
+
+    def set_window_size(self, window_size) -> None:
+        if isinstance(window_size, int):
+            window_size = (window_size, window_size)
+        window_size = tuple(int(x) for x in window_size)
+        if window_size == self.window_size:
+            return
+        self.window_size = window_size
+        win_h, win_w = window_size
+        self.window_area = win_h * win_w
+        with torch.no_grad():
+            self.relative_position_bias_table = nn.Parameter(
+                resize_rel_pos_bias_table(self.relative_position_bias_table, window_size))
+            self.register_buffer("relative_position_index",
+                                 relative_position_index(win_h, win_w, device=self.relative_position_bias_table.device),
+                                 persistent=False)
+
+    def _qkv_and_bias(self, x: torch.Tensor, mask: Optional[torch.Tensor]):
+        batch_windows, seq_len, _ = x.shape
+        qkv = self.qkv(x).reshape(batch_windows, seq_len, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4)
+        q, k, v = qkv.unbind(0)
+        canonical_scale = self.head_dim ** -0.5
+        if abs(self.scale - canonical_scale) > 1e-12:
+            q = q * (self.scale / canonical_scale)
+        bias = self._get_rel_pos_bias()
+        if mask is not None:
+            num_win = int(mask.shape[0])
+            mask_bias = mask.view(1, num_win, 1, seq_len, seq_len).expand(
+                batch_windows // num_win, -1, self.num_heads, -1, -1)
+            bias = bias + mask_bias.reshape(-1, self.num_heads, seq_len, seq_len)
+        return q, k, v, bias
+
+    def _out(self, y: torch.Tensor, batch_windows: int, seq_len: int) -> torch.Tensor:
+        y = y.transpose(1, 2).reshape(batch_windows, seq_len, self.attn_dim)
+        return self.proj_drop(self.proj(y))
+
+
+class ElsaTimmSwinWindowAttention(_SwinWindowCommon):
+    def __init__(self, source: nn.Module, *, elsa_kwargs: Optional[dict] = None) -> None:
+        super().__init__()
+        _swin_state(self, source, elsa_kwargs)
+
+    def _elsa_kwargs_for_window(self, seq_len: int) -> dict:
+        kwargs = dict(self.elsa_kwargs)
+        kwargs["algorithm"] = "paper_scan"
+        kwargs.setdefault("block_m", 64)
+        kwargs.setdefault("block_n", 64)
+        kwargs.setdefault("q_chunk_size", seq_len)
+        return kwargs
+
+    def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if self.training and self.attn_drop.p:
+            raise ValueError("ELSA Swin drop-in forward is inference-only when attention dropout is nonzero")
+        q, k, v, bias = self._qkv_and_bias(x, mask)
+        y = twopass_attention(q, k, v, bias=bias, **self._elsa_kwargs_for_window(x.shape[1]))
+        return self._out(y, x.shape[0], x.shape[1])
+
+
+def _is_vit_attention(module: nn.Module) -> bool:
+    required = ("qkv", "q_norm", "k_norm", "proj", "num_heads", "head_dim")
+    return all(hasattr(module, name) for name in required)
+
+
+def _is_swin_v1_window_attention(module: nn.Module) -> bool:
+    required = ("qkv", "proj", "relative_position_bias_table", "relative_position_index", "window_area",
+                "window_size", "scale", "num_heads", "dim")
+    return all(hasattr(module, name) for name in required) and not hasattr(module, "logit_scale")
+
+
+def _patch(model: nn.Module, vit_cls, swin_cls, elsa_kwargs: Optional[dict]) -> tuple[int, int]:
+    vit_count = 0
+    swin_count = 0
+
+    def visit(parent: nn.Module) -> None:
+        nonlocal vit_count, swin_count
+        for name, child in list(parent.named_children()):
+            if _is_vit_attention(child):
+                setattr(parent, name, vit_cls(child, elsa_kwargs=elsa_kwargs))
+                vit_count += 1
+            elif _is_swin_v1_window_attention(child):
+                setattr(parent, name, swin_cls(child, elsa_kwargs=elsa_kwargs))
+                swin_count += 1
+            else:
+                visit(child)
+
+    visit(model)
+    if vit_count + swin_count == 0:
+        raise ValueError("no compatible timm ViT or Swin v1 attention modules were patched")
+    return vit_count, swin_count
+
+
+def patch_timm_attention(model: nn.Module, *, elsa_kwargs: Optional[dict] = None) -> PatchReport:
+    """Replace every timm ViT / Swin v1 attention module in ``model`` (in place)."""
+    vit, swin = _patch(model, ElsaTimmVitAttention, ElsaTimmSwinWindowAttention, elsa_kwargs)
+    return PatchReport(vit_attention=vit, swin_window_attention=swin)

@@ -1,0 +1,106 @@
+"""GPU tests of the callers of the path: ViT-T / Swin-T with the ELSA drop-ins against the
+same models on PyTorch SDPA (forward and gradients), the reference's toy-encoder pair
+test (tests/test_attention.py:116-130), and a hipGraph capture of the patched forward
+replayed several times with eager work in between."""
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+import elsa_amd
+from elsa_amd.vision_models import swin_tiny_patch4_window7, vit_tiny_patch16
+from tests.gpu_util import describe
+
+pytestmark = pytest.mark.gpu
+
+
+def _models(builder, img, dtype, train=False):
+    torch.manual_seed(1234)
+    base = builder(img).eval()
+    elsa = copy.deepcopy(base)
+    (elsa_amd.patch_timm_attention_train if train else elsa_amd.patch_timm_attention)(elsa)
+    ref32 = copy.deepcopy(base).to("cuda", torch.float32)
+    return ref32, elsa.to("cuda", dtype)
+
+
+@pytest.mark.parametrize("dt,tol", [(torch.float32, 2e-4), (torch.float16, 2e-2)])
+@pytest.mark.parametrize("builder,img", [(vit_tiny_patch16, 224), (swin_tiny_patch4_window7, 224),
+                                         (vit_tiny_patch16, 512)])
+def test_dropin_forward_matches_sdpa(builder, img, dt, tol):
+    describe(f"dropin fwd {builder.__name__} {img} {dt}")
+    ref, elsa = _models(builder, img, dt)
+    x = torch.randn(2, 3, img, img, generator=torch.Generator().manual_seed(7)).cuda()
+    with torch.no_grad():
+        want = ref(x)
+        got = elsa(x.to(dt)).float()
+    err = (got - want).abs().max().item()
+    describe(f"  max_abs logits {err:.3e}")
+    assert err <= tol * max(1.0, want.abs().max().item())
+
+
+@pytest.mark.parametrize("builder,img", [(vit_tiny_patch16, 224), (swin_tiny_patch4_window7, 224)])
+def test_dropin_training_gradients_match_sdpa(builder, img):
+    describe(f"dropin train {builder.__name__} {img}")
+    ref, elsa = _models(builder, img, torch.float32, train=True)
+    ref.train()
+    elsa.train()
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(2, 3, img, img, generator=g).cuda()
+    labels = torch.randint(0, 1000, (2,), generator=g).cuda()
+    for m in (ref, elsa):
+        torch.nn.functional.cross_entropy(m(x), labels).backward()
+    worst = 0.0
+    for (n, p), (_, q) in zip(ref.named_parameters(), elsa.named_parameters()):
+        assert p.grad is not None and q.grad is not None, n
+        err = (p.grad - q.grad).abs().max().item() / max(1e-6, p.grad.abs().max().item())
+        worst = max(worst, err)
+        assert err <= 2e-3, (n, err)
+    describe(f"  worst relative grad error {worst:.3e}")
+
+
+@pytest.mark.parametrize("dt,tol", [(torch.float32, 5e-3), (torch.float16, 8e-2)])
+def test_full_model_pair_matches(dt, tol):
+    torch.manual_seed(6)
+    baseline, elsa = elsa_amd.make_model_pair(dim=96, depth=2, heads=3)
+    baseline = baseline.eval().to(device="cuda", dtype=dt)
+    elsa = elsa.eval().to(device="cuda", dtype=dt)
+    x = torch.randn((1, 128, 96), device="cuda", dtype=dt)
+    with torch.no_grad():
+        torch.testing.assert_close(elsa(x), baseline(x), atol=tol, rtol=tol)
+
+
+def test_train_model_pair_gradients():
+    torch.manual_seed(7)
+    base, elsa = elsa_amd.make_train_model_pair(dim=96, depth=2, heads=3, is_causal=True)
+    base, elsa = base.cuda(), elsa.cuda()
+    x = torch.randn((2, 200, 96), device="cuda")
+    for m in (base, elsa):
+        m(x).square().mean().backward()
+    for (n, p), (_, q) in zip(base.named_parameters(), elsa.named_parameters()):
+        torch.testing.assert_close(q.grad, p.grad, atol=5e-5, rtol=5e-3, msg=n)
+
+
+def test_hipgraph_capture_of_patched_forward_replays():
+    describe("hipgraph capture")
+    _, elsa = _models(vit_tiny_patch16, 224, torch.float16)
+    static_x = torch.randn(4, 3, 224, 224, device="cuda", dtype=torch.float16)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s), torch.no_grad():
+        for _ in range(2):
+            elsa(static_x)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.graph(graph):
+        static_y = elsa(static_x)
+    for i in range(4):
+        static_x.copy_(torch.randn_like(static_x))
+        graph.replay()
+        torch.cuda.synchronize()
+        with torch.no_grad():
+            eager = elsa(static_x)
+        torch.cuda.synchronize()
+        assert torch.equal(static_y, eager), i

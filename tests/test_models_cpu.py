@@ -1,0 +1,103 @@
+"""CPU tests of the drop-in layer: duck typing, patch counts, copied state, Swin window
+geometry and masks, and the toy-encoder pairs (no kernel launches)."""
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn as nn
+
+import elsa_amd
+from elsa_amd.timm_dropin import ElsaTimmSwinWindowAttention, ElsaTimmVitAttention
+from elsa_amd.timm_dropin_bwd import ElsaTrainTimmSwinWindowAttention, ElsaTrainTimmVitAttention
+from elsa_amd.vision_models import (SwinTransformerBlock, relative_position_index, swin_tiny_patch4_window7,
+                                    vit_tiny_patch16)
+
+
+def test_vit_tiny_patch_counts_and_state():
+    torch.manual_seed(0)
+    m = vit_tiny_patch16(224)
+    ref_qkv = m.blocks[3].attn.qkv.weight.detach().clone()
+    rep = elsa_amd.patch_timm_attention(m)
+    assert rep == elsa_amd.PatchReport(vit_attention=12, swin_window_attention=0) and rep.total == 12
+    a = m.blocks[3].attn
+    assert isinstance(a, ElsaTimmVitAttention) and a.num_heads == 3 and a.head_dim == 64 and a.attn_dim == 192
+    assert torch.equal(a.qkv.weight, ref_qkv)
+
+
+def test_swin_tiny_patch_counts_train():
+    m = swin_tiny_patch4_window7(224)
+    rep = elsa_amd.patch_timm_attention_train(m)
+    assert rep == elsa_amd.TrainPatchReport(vit_attention=0, swin_window_attention=12)
+    assert isinstance(m.layers[2].blocks[5].attn, ElsaTrainTimmSwinWindowAttention)
+    assert m.layers[2].blocks[5].attn.head_dim == 32
+
+
+def test_patch_rejects_models_without_attention():
+    with pytest.raises(ValueError, match="no compatible timm"):
+        elsa_amd.patch_timm_attention(nn.Sequential(nn.Linear(4, 4)))
+    with pytest.raises(ValueError, match="no compatible timm"):
+        elsa_amd.patch_timm_attention_train(nn.Sequential(nn.Linear(4, 4)))
+
+
+def test_swin_v2_style_module_is_not_patched():
+    m = swin_tiny_patch4_window7(224)
+    m.layers[0].blocks[0].attn.logit_scale = nn.Parameter(torch.zeros(3, 1, 1))
+    rep = elsa_amd.patch_timm_attention(m)
+    assert rep.swin_window_attention == 11
+
+
+def test_vit_dropin_rejects_mask_and_dropout():
+    m = vit_tiny_patch16(224)
+    elsa_amd.patch_timm_attention(m)
+    with pytest.raises(ValueError, match="unmasked"):
+        m.blocks[0].attn(torch.zeros(1, 197, 192), attn_mask=torch.zeros(197, 197))
+    t = vit_tiny_patch16(224)
+    t.blocks[0].attn.attn_drop.p = 0.1
+    elsa_amd.patch_timm_attention_train(t)
+    t.train()
+    with pytest.raises(ValueError, match="dropout"):
+        t.blocks[0].attn(torch.zeros(1, 197, 192))
+
+
+def test_relative_position_index_closed_form():
+    idx = relative_position_index(2, 3)
+    # (dy + 1) * 5 + (dx + 2) for query (y1,x1), key (y2,x2), dy = y1 - y2, dx = x1 - x2
+    coords = [(y, x) for y in range(2) for x in range(3)]
+    for i, (y1, x1) in enumerate(coords):
+        for j, (y2, x2) in enumerate(coords):
+            assert idx[i, j] == (y1 - y2 + 1) * 5 + (x1 - x2 + 2)
+
+
+def test_shifted_window_mask_values():
+    blk = SwinTransformerBlock(96, (14, 14), 3, 7, shift=True)
+    assert blk.shift_size == (3, 3)
+    mask = blk.attn_mask
+    assert mask.shape == (4, 49, 49)
+    assert set(mask.unique().tolist()) == {0.0, -100.0}
+    assert torch.all(mask[0] == 0)  # top-left window is not split by the shift
+    no_shift = SwinTransformerBlock(96, (7, 7), 3, 7, shift=True)
+    assert no_shift.shift_size == (0, 0) and no_shift.attn_mask is None
+
+
+def test_set_window_size_resizes_table_and_index():
+    m = swin_tiny_patch4_window7(224)
+    elsa_amd.patch_timm_attention(m)
+    a = m.layers[0].blocks[0].attn
+    assert isinstance(a, ElsaTimmSwinWindowAttention)
+    a.set_window_size(8)
+    assert a.window_size == (8, 8) and a.window_area == 64
+    assert a.relative_position_bias_table.shape == (15 * 15, 3)
+    assert a.relative_position_index.shape == (64, 64) and int(a.relative_position_index.max()) == 15 * 15 - 1
+
+
+def test_model_pairs_share_weights():
+    base, elsa = elsa_amd.make_model_pair(dim=96, depth=2, heads=3)
+    for (n1, p1), (n2, p2) in zip(base.state_dict().items(), elsa.state_dict().items()):
+        assert n1 == n2 and torch.equal(p1, p2)
+    assert base.blocks[0].attn.backend == "sdpa" and elsa.blocks[0].attn.backend == "elsa"
+    tb, te = elsa_amd.make_train_model_pair(dim=96, depth=1, heads=3)
+    assert isinstance(te, elsa_amd.TrainableTransformerEncoder)
+    x = torch.randn(1, 16, 96)
+    assert base(x).shape == (1, 16, 96) and tb(x).shape == (1, 16, 96)
+    with pytest.raises(ValueError, match="divisible"):
+        elsa_amd.make_model_pair(dim=95, heads=3)
