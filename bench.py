@@ -48,8 +48,68 @@ def _args():
     ap.add_argument("--cpu-rows", type=int, default=512, help="query rows of the CPU-baseline sample")
     ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "traffic_north_star.json"))
     ap.add_argument("--copy-mib", type=int, default=0,
-                    help="after timing, run one device-to-device copy of this many MiB (HBM-counter calibration)")
+                    help="after timing, run one copy kernel over this many MiB (HBM-counter calibration)")
+    ap.add_argument("--vit-img", type=int, nargs="*", default=[224, 1024],
+                    help="ViT-Tiny image sizes for the img/s fields (empty: skip)")
+    ap.add_argument("--vit-batch", type=int, default=8)
+    ap.add_argument("--vit-steps", type=int, default=10)
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="no GPU work: turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, "
+                         "WRITE_SIZE) of a --copy-mib run into per-launch HBM bytes, written to --traffic-file")
     return ap.parse_args()
+
+
+# rocprofv3 kernel-name fragment -> bench kernel name
+_KERNEL_KEYS = (("phase1_half_kernel", "phase1_fold"), ("phase1_kernel", "phase1_fold"),
+                ("phase2_kernel", "phase2_merge"), ("bwd_pre_kernel", "bwd_preprocess"),
+                ("bwd_dq_half_kernel", "bwd_dq"), ("bwd_dq_kernel", "bwd_dq"),
+                ("bwd_dkdv_half_kernel", "bwd_dkdv"), ("bwd_dkdv_kernel", "bwd_dkdv"))
+
+
+def _read_pmc(path, counter):
+    import csv
+
+    rows = []
+    with open(path, newline="") as fh:
+        for r in csv.DictReader(fh):
+            if r["Counter_Name"] == counter:
+                rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return rows
+
+
+def summarize_pmc(fetch_csv, write_csv, copy_mib, out_path):
+    """Per-launch HBM bytes of each ELSA kernel from FETCH_SIZE / WRITE_SIZE (KiB per dispatch).
+
+    Each counter is scaled by what it reads for the calibration kernel of the same run
+    (``torch.add`` over ``copy_mib`` MiB of fp32: copy_mib MiB read and copy_mib MiB written,
+    the last elementwise add dispatch), so the figures are bytes, whatever fraction of the
+    memory channels the counter samples.
+    """
+    out = {"copy_calibration_mib": copy_mib}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = _read_pmc(path, counter)
+        cal = [v for _, name, v in rows if "add" in name.lower() and "elementwise" in name.lower()]
+        if not cal or cal[-1] <= 0:
+            raise SystemExit(f"{path}: no calibration add kernel with a positive {counter}")
+        factor = copy_mib * 1024.0 / cal[-1]
+        out[f"{counter.lower()}_factor"] = round(factor, 4)
+        per = {}
+        for _, name, v in rows:
+            key = next((b for frag, b in _KERNEL_KEYS if frag in name), None)
+            if key is not None:
+                per.setdefault(key, []).append(v * factor * 1024.0)
+        for key, vals in per.items():
+            ent = out.setdefault(key, {})
+            ent[counter.lower() + "_bytes"] = sum(vals) / len(vals)
+            ent["dispatches"] = len(vals)
+    for key, ent in out.items():
+        if isinstance(ent, dict) and "fetch_size_bytes" in ent and "write_size_bytes" in ent:
+            ent["hbm_bytes_per_launch"] = round(ent["fetch_size_bytes"] + ent["write_size_bytes"])
+    with open(out_path, "w") as fh:
+        json.dump(out, fh, indent=1, sort_keys=True)
+        fh.write("\n")
+    return out
 
 
 def _flops_fwd(b, h, n, d, causal):
@@ -58,6 +118,10 @@ def _flops_fwd(b, h, n, d, causal):
 
 def main() -> int:
     args = _args()
+    if args.summarize_pmc:
+        res = summarize_pmc(*args.summarize_pmc, args.copy_mib or 1024, args.traffic_file)
+        print(json.dumps(res))
+        return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures a single GPU: this build has no multi-GPU path (the attention shards by "
@@ -231,17 +295,114 @@ def main() -> int:
         "kernels": kernels,
         "roofline": roofline,
     }
+    if args.vit_img:
+        result["vit_tiny"] = _vit_bench(args, dt)
     if args.copy_mib > 0:
-        src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        # one elementwise kernel that reads and writes copy_mib MiB each: the FETCH_SIZE / WRITE_SIZE
+        # calibration for the HBM-traffic figures
+        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
-        dst.copy_(src)
+        torch.add(src, 1.0, out=dst)
         torch.cuda.synchronize()
         result["copy_calibration_mib"] = args.copy_mib
     if args.cpu_baseline:
         result["cpu_baseline"] = _cpu_baseline(args, B, H, N, D, causal)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def _vit_bench(args, dt):
+    """ViT-Tiny img/s with the ELSA drop-in against the same model on PyTorch SDPA.
+
+    Follows the reference's model benchmarks (benchmarks/full_model_graph.py,
+    benchmarks/full_model_bwd_min.py): random-init weights cast to the compute dtype, a
+    synthetic N(0,1) image batch, forward timed as hipGraph replays, and a training step
+    of forward, cross-entropy on synthetic labels over 1000 classes, backward and an SGD
+    update.  Times are means over the timed iterations.
+    """
+    import copy
+
+    import torch
+
+    import elsa_amd
+    from elsa_amd.vision_models import vit_tiny_patch16
+
+    out = {"model": "vit_tiny_patch16 (embed 192, depth 12, heads 3, d 64), random init", "batch": args.vit_batch}
+    for img in args.vit_img:
+        torch.manual_seed(2468 + img)
+        base = vit_tiny_patch16(img)
+        elsa_fwd = copy.deepcopy(base)
+        elsa_amd.patch_timm_attention(elsa_fwd)
+        elsa_train = copy.deepcopy(base)
+        elsa_amd.patch_timm_attention_train(elsa_train)
+        models = {"sdpa": base.to("cuda", dt), "elsa": elsa_fwd.to("cuda", dt)}
+        x = torch.randn(args.vit_batch, 3, img, img, device="cuda", dtype=dt)
+        labels = torch.randint(0, 1000, (args.vit_batch,), device="cuda")
+        row = {"tokens": (img // 16) ** 2 + 1}
+        for name, m in models.items():
+            m.eval()
+            row[f"{name}_fwd_ms"] = _graph_fwd_ms(m, x, args.vit_steps)
+        for name, m in (("sdpa", models["sdpa"]), ("elsa", elsa_train.to("cuda", dt))):
+            row[f"{name}_train_ms"] = _train_ms(m, x, labels, args.vit_steps)
+        for kind in ("fwd", "train"):
+            row[f"elsa_{kind}_img_s"] = round(args.vit_batch / (row[f"elsa_{kind}_ms"] * 1e-3), 1)
+            row[f"{kind}_lat_ratio_vs_sdpa"] = round(row[f"elsa_{kind}_ms"] / row[f"sdpa_{kind}_ms"], 3)
+        print(f"bench: vit_tiny {img}px {row}", file=sys.stderr, flush=True)
+        out[str(img)] = row
+        del models, elsa_train
+        torch.cuda.empty_cache()
+    return out
+
+
+def _graph_fwd_ms(model, x, steps):
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s), torch.no_grad():
+        for _ in range(3):
+            model(x)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.graph(graph):
+        model(x)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    del graph
+    return round(ms, 4)
+
+
+def _train_ms(model, x, labels, steps):
+    import torch
+
+    model.train()
+    opt = torch.optim.SGD(model.parameters(), lr=1e-4, momentum=0.9)
+
+    def one():
+        opt.zero_grad(set_to_none=True)
+        loss = torch.nn.functional.cross_entropy(model(x).float(), labels)
+        loss.backward()
+        opt.step()
+
+    for _ in range(3):
+        one()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        one()
+    e1.record()
+    torch.cuda.synchronize()
+    return round(e0.elapsed_time(e1) / steps, 4)
 
 
 def _cpu_baseline(args, B, H, N, D, causal):

@@ -118,8 +118,9 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
-  const int bh = blockIdx.y;
-  const int wg_row0 = blockIdx.x * BM;
+  const WgCoord wg = xcd_order();
+  const int bh = wg.y;
+  const int wg_row0 = wg.x * BM;
   const int wg_last = min(p.N, wg_row0 + BM) - 1;
   const int my_row = wg_row0 + wave * 32 + c;
   const bool row_ok = my_row < p.N;
@@ -209,8 +210,9 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dkdv_kernel(const BwdParams p)
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
-  const int bh = blockIdx.y;
-  const int wg_key0 = blockIdx.x * BN;
+  const WgCoord wg = xcd_order();
+  const int bh = wg.y;
+  const int wg_key0 = wg.x * BN;
   const int key0 = wg_key0 + wave * 32;
   const int my_key = key0 + c;
   const bool key_ok = my_key < p.N;
@@ -340,8 +342,9 @@ void bwd_dq_half_kernel(const BwdParams p) {
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
-  const int bh = blockIdx.y;
-  const int wg_row0 = blockIdx.x * BM;
+  const WgCoord wg = xcd_order();
+  const int bh = wg.y;
+  const int wg_row0 = wg.x * BM;
   const int wg_last = min(p.N, wg_row0 + BM) - 1;
   const int row0 = wg_row0 + wave * ROWS_W;
   const int64_t hoff = (int64_t)bh * p.N * p.D;
@@ -375,8 +378,8 @@ void bwd_dq_half_kernel(const BwdParams p) {
 
   Chunk16 kreg[NCH], vreg[NCH];
   auto gload = [&](int t0) {
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
+static_for<0, NCH>([&](auto I) {
+      constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
       if (t0 + r < k_end && d0 < p.D) {
@@ -387,16 +390,16 @@ void bwd_dq_half_kernel(const BwdParams p) {
         kreg[i] = Chunk16{};
         vreg[i] = Chunk16{};
       }
-    }
+    });
   };
   auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
+static_for<0, NCH>([&](auto I) {
+      constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
       *reinterpret_cast<Chunk16*>(&Ks[buf][r * KS + d0]) = kreg[i];
       *reinterpret_cast<Chunk16*>(&Vs[buf][r * KS + d0]) = vreg[i];
-    }
+    });
   };
 
   f32x16 acc[RT][NDT];
@@ -520,8 +523,9 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
-  const int bh = blockIdx.y;
-  const int wg_key0 = blockIdx.x * BN;
+  const WgCoord wg = xcd_order();
+  const int bh = wg.y;
+  const int wg_key0 = wg.x * BN;
   const int key0 = wg_key0 + wave * KEYS_W;
   const int64_t hoff = (int64_t)bh * p.N * p.D;
   const T* Q = static_cast<const T*>(p.q) + hoff;
@@ -558,8 +562,8 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
   Chunk16 qreg[NCH], greg[NCH];
   float lreg = 0.f, dreg = 0.f;
   auto gload = [&](int t0) {
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
+static_for<0, NCH>([&](auto I) {
+      constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
       if (t0 + r < p.N && d0 < p.D) {
@@ -570,7 +574,7 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
         qreg[i] = Chunk16{};
         greg[i] = Chunk16{};
       }
-    }
+    });
     if (tid < RTS) {  // rows past N: LSE2 = +inf makes their p exactly 0
       const int ra = t0 + tid;
       lreg = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : __builtin_huge_valf();
@@ -578,13 +582,13 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
     }
   };
   auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
+static_for<0, NCH>([&](auto I) {
+      constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
       *reinterpret_cast<Chunk16*>(&Qs[buf][r * KS + d0]) = qreg[i];
       *reinterpret_cast<Chunk16*>(&Gs[buf][r * KS + d0]) = greg[i];
-    }
+    });
     if (tid < RTS) {
       lse_s[buf][tid] = lreg;
       dd_s[buf][tid] = dreg;
@@ -715,8 +719,9 @@ __global__ __launch_bounds__(64 * WAVES) void row_stats_kernel(const BwdParams p
   __shared__ __attribute__((aligned(16))) T Kt[C::HALF ? 1 : DP * C::TS];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
-  const int bh = blockIdx.y;
-  const int wg_row0 = blockIdx.x * BM;
+  const WgCoord wg = xcd_order();
+  const int bh = wg.y;
+  const int wg_row0 = wg.x * BM;
   const int wg_last = min(p.N, wg_row0 + BM) - 1;
   const int my_row = wg_row0 + wave * 32 + c;
   const bool row_ok = my_row < p.N;

@@ -93,9 +93,10 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31, g = lane >> 5;
-  const int bh = blockIdx.y, kb = blockIdx.z;
+  const WgCoord wg = xcd_order();
+  const int bh = wg.y, kb = wg.z;
   const int q_end = p.q_start + p.q_len;
-  const int wg_row0 = p.q_start + blockIdx.x * BM;
+  const int wg_row0 = p.q_start + wg.x * BM;
   const int wg_last = min(q_end, wg_row0 + BM) - 1;
   const int k_begin = kb * p.part_len;
   int k_end = min(p.N, k_begin + p.part_len);
@@ -317,9 +318,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31, g = lane >> 5;
-  const int bh = blockIdx.y, kb = blockIdx.z;
+  const WgCoord wg = xcd_order();
+  const int bh = wg.y, kb = wg.z;
   const int q_end = p.q_start + p.q_len;
-  const int wg_row0 = p.q_start + blockIdx.x * BM;
+  const int wg_row0 = p.q_start + wg.x * BM;
   const int wg_last = min(q_end, wg_row0 + BM) - 1;
   const int k_begin = kb * p.part_len;
   int k_end = min(p.N, k_begin + p.part_len);
@@ -351,8 +353,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 
   Chunk16 kreg[NCH], vreg[NCH];
   auto gload = [&](int t0) {
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
+    static_for<0, NCH>([&](auto I) {
+      constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int key = ci / CPR, d0 = (ci % CPR) * 8;
       const int ka = t0 + key;
@@ -364,16 +366,16 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         kreg[i] = Chunk16{};
         vreg[i] = Chunk16{};
       }
-    }
+    });
   };
   auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
+    static_for<0, NCH>([&](auto I) {
+      constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int key = ci / CPR, d0 = (ci % CPR) * 8;
       *reinterpret_cast<Chunk16*>(&Ks[buf][key * KS + d0]) = kreg[i];
       *reinterpret_cast<Chunk16*>(&Vs[buf][key * KS + d0]) = vreg[i];
-    }
+    });
   };
 
   f32x16 oacc[RT][NDT];

@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace elsa {
 
 typedef _Float16 f16;
@@ -109,10 +111,22 @@ __device__ inline typename Mfma<T>::frag pack_frag(const f32x16& v) {
   }
 }
 
-// 16-byte raw chunk used for global->LDS staging.
-struct alignas(16) Chunk16 {
-  uint32_t w[4];
-};
+// Compile-time loop: f(std::integral_constant<int, I>) for I = B .. E-1.  Register
+// staging arrays indexed through it see constant indices from the start, so they are
+// split into VGPRs; indexed by a `#pragma unroll` loop variable they can instead be
+// placed in LDS or scratch before the loop is unrolled.
+template <int B, int E, typename Fn>
+__device__ inline void static_for(Fn&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// 16-byte raw chunk used for global->LDS staging.  A vector type, not a struct: a
+// struct copy is a memcpy, and a staging array of structs copied global -> array ->
+// LDS by memcpy is not split into registers (it ends up in LDS or scratch).
+typedef uint32_t Chunk16 __attribute__((ext_vector_type(4)));
 
 // acc + a + b with an fp32 accumulator (v_dot2_f32_f16 / v_dot2_f32_bf16 against (1, 1)).
 __device__ inline float sum2(f16 a, f16 b, float acc) {
@@ -131,6 +145,24 @@ __device__ inline float sum2(bf16 a, bf16 b, float acc) {
 // lane i the column segment M[k0 .. k0+3][d0 + i].
 __device__ inline i16x4 lds_read_tr16(const void* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)p);
+}
+
+// Work-group coordinates in an XCD-aware order.  The dispatcher hands the work-groups
+// of a launch (x fastest, then y, then z) to the 8 XCDs round-robin, and each XCD has
+// its own L2.  Renumbering so that the work-groups running on one XCD cover one
+// contiguous range of the logical grid (x fastest) keeps the K/V panel that neighbouring
+// row blocks share in one L2, instead of fetching it into all eight.  The map is a
+// bijection for any grid size.
+struct WgCoord {
+  int x, y, z;
+};
+__device__ inline WgCoord xcd_order() {
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int n = gx * gy * gridDim.z;
+  const int lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const int per = n >> 3, rem = n & 7, xcd = lin & 7, slot = lin >> 3;
+  const int l = xcd * per + min(xcd, rem) + slot;
+  return {l % gx, (l / gx) % gy, l / (gx * gy)};
 }
 
 // Combine the two 32-lane halves of a wave (lanes l and l ^ 32) with
