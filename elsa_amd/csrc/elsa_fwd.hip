@@ -294,7 +294,7 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
 // LDS load.  The running max is lazy: it is raised only when a 64-key stage
 // exceeds it by more than kLazyTau (p stays <= 2^kLazyTau, exact in fp16/bf16 and
 // fp32), and the summary is renormalised to the exact row maximum at the end.
-// The row sum accumulates the same 16-bit p values that feed the MFMA.
+// The row sum accumulates the fp32 p values; the MFMA takes them rounded to T.
 constexpr float kLazyTau = 8.0f;
 
 template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS>
@@ -351,21 +351,25 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
+  // K/V of this partition through buffer resources: keys past k_end and head-dim
+  // padding (d0 >= D) read as zeros
+  const uint32_t part_bytes = (uint32_t)(k_end - k_begin) * (uint32_t)p.D * (uint32_t)sizeof(T);
+  const auto rk = make_rsrc(K + (int64_t)k_begin * p.D, part_bytes);
+  const auto rv = make_rsrc(V + (int64_t)k_begin * p.D, part_bytes);
+  uint32_t voff[NCH];
+  static_for<0, NCH>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    const int ci = tid + i * NT;
+    const int key = ci / CPR, d0 = (ci % CPR) * 8;
+    voff[i] = d0 < p.D ? (uint32_t)(key * p.D + d0) * (uint32_t)sizeof(T) : kBufferOff;
+  });
   Chunk16 kreg[NCH], vreg[NCH];
   auto gload = [&](int t0) {
+    const uint32_t soff = (uint32_t)(t0 - k_begin) * (uint32_t)p.D * (uint32_t)sizeof(T);
     static_for<0, NCH>([&](auto I) {
       constexpr int i = decltype(I)::value;
-      const int ci = tid + i * NT;
-      const int key = ci / CPR, d0 = (ci % CPR) * 8;
-      const int ka = t0 + key;
-      if (ka < k_end && d0 < p.D) {
-        const int64_t off = (int64_t)ka * p.D + d0;
-        kreg[i] = *reinterpret_cast<const Chunk16*>(K + off);
-        vreg[i] = *reinterpret_cast<const Chunk16*>(V + off);
-      } else {
-        kreg[i] = Chunk16{};
-        vreg[i] = Chunk16{};
-      }
+      kreg[i] = buffer_load16(rk, voff[i], soff);
+      vreg[i] = buffer_load16(rv, voff[i], soff);
     });
   };
   auto sstore = [&](int buf) {
@@ -450,10 +454,15 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
                 if (!(key < k_end && (!p.causal || key <= my_row))) s[rt][sub][r] = kNegInf;
               }
           }
+          float mx1 = kNegInf;  // two v_max3 chains
 #pragma unroll
           for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[rt][sub][r], s[rt][sub][r + 1]));
+            for (int r = 0; r < 16; r += 4) {
+              mx = fmaxf(fmaxf(mx, s[rt][sub][r]), s[rt][sub][r + 1]);
+              mx1 = fmaxf(fmaxf(mx1, s[rt][sub][r + 2]), s[rt][sub][r + 3]);
+            }
+          mx = fmaxf(mx, mx1);
         }
         mx = wave_max_pair(mx);
         m_tile[rt] = HAS_BIAS ? mx : mx * cs;

@@ -128,6 +128,18 @@ __device__ inline void static_for(Fn&& f) {
 // LDS by memcpy is not split into registers (it ends up in LDS or scratch).
 typedef uint32_t Chunk16 __attribute__((ext_vector_type(4)));
 
+// Raw buffer resource over [base, base + bytes): loads at offsets >= bytes return
+// zeros, which is the key-range masking the tile loaders need, with no per-chunk
+// address arithmetic or compare in VGPRs.  bytes must stay below 2^31 so that an
+// offset pushed past it by kBufferOff never wraps.
+constexpr uint32_t kBufferOff = 0x80000000u;
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+__device__ inline Chunk16 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(Chunk16, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
 // acc + a + b with an fp32 accumulator (v_dot2_f32_f16 / v_dot2_f32_bf16 against (1, 1)).
 __device__ inline float sum2(f16 a, f16 b, float acc) {
   const f16x2 v = {a, b}, one = {(f16)1.0f, (f16)1.0f};
