@@ -34,8 +34,8 @@ HBM_GBPS = 8000.0
 def _args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--heads", type=int, default=8)
     ap.add_argument("--seq", type=int, default=16384)
@@ -45,7 +45,7 @@ def _args():
     ap.add_argument("--block-n", type=int, default=None, help="K-partition width (default: planner)")
     ap.add_argument("--cpu-baseline", dest="cpu_baseline", action="store_true", default=True)
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
-    ap.add_argument("--cpu-rows", type=int, default=512, help="query rows of the CPU-baseline sample")
+    ap.add_argument("--cpu-rows", type=int, default=1536, help="query rows of the CPU-baseline sample")
     ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "traffic_north_star.json"))
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after timing, run one copy kernel over this many MiB (HBM-counter calibration)")
@@ -124,8 +124,8 @@ def main() -> int:
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures a single GPU: this build has no multi-GPU path (the attention shards by "
-              "heads with no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr, flush=True)
+        print("bench.py measures a single GPU: this build has no multi-GPU path (the attention would shard "
+              "by batch x heads with no communication). Run with --gpus 1.", file=sys.stderr, flush=True)
         return 2
 
     import numpy as np
