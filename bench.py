@@ -51,8 +51,10 @@ def _args():
                     help="after timing, run one copy kernel over this many MiB (HBM-counter calibration)")
     ap.add_argument("--vit-img", type=int, nargs="*", default=[224, 1024],
                     help="ViT-Tiny image sizes for the img/s fields (empty: skip)")
-    ap.add_argument("--vit-batch", type=int, default=8)
-    ap.add_argument("--vit-steps", type=int, default=10)
+    ap.add_argument("--swin-img", type=int, nargs="*", default=[224],
+                    help="Swin-Tiny image sizes for the img/s fields (empty: skip)")
+    ap.add_argument("--vit-batch", type=int, default=8, help="image batch of the ViT-T / Swin-T fields")
+    ap.add_argument("--vit-steps", type=int, default=10, help="timed iterations of the ViT-T / Swin-T fields")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="no GPU work: turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, "
                          "WRITE_SIZE) of a --copy-mib run into per-launch HBM bytes, written to --traffic-file")
@@ -296,7 +298,17 @@ def main() -> int:
         "roofline": roofline,
     }
     if args.vit_img:
-        result["vit_tiny"] = _vit_bench(args, dt)
+        from elsa_amd.vision_models import vit_tiny_patch16
+
+        result["vit_tiny"] = _vision_bench(args, dt, vit_tiny_patch16, args.vit_img,
+                                           "vit_tiny_patch16 (embed 192, depth 12, heads 3, d 64), random init",
+                                           lambda img: (img // 16) ** 2 + 1)
+    if args.swin_img:
+        from elsa_amd.vision_models import swin_tiny_patch4_window7
+
+        result["swin_tiny"] = _vision_bench(args, dt, swin_tiny_patch4_window7, args.swin_img,
+                                            "swin_tiny_patch4_window7 (embed 96, depths 2-2-6-2, heads 3-6-12-24, "
+                                            "d 32, window 7), random init", lambda img: 49)
     if args.copy_mib > 0:
         # one elementwise kernel that reads and writes copy_mib MiB each: the FETCH_SIZE / WRITE_SIZE
         # calibration for the HBM-traffic figures
@@ -312,8 +324,8 @@ def main() -> int:
     return 0
 
 
-def _vit_bench(args, dt):
-    """ViT-Tiny img/s with the ELSA drop-in against the same model on PyTorch SDPA.
+def _vision_bench(args, dt, builder, imgs, label, tokens):
+    """img/s of a vision model with the ELSA drop-in against the same model on PyTorch SDPA.
 
     Follows the reference's model benchmarks (benchmarks/full_model_graph.py,
     benchmarks/full_model_bwd_min.py): random-init weights cast to the compute dtype, a
@@ -326,12 +338,11 @@ def _vit_bench(args, dt):
     import torch
 
     import elsa_amd
-    from elsa_amd.vision_models import vit_tiny_patch16
 
-    out = {"model": "vit_tiny_patch16 (embed 192, depth 12, heads 3, d 64), random init", "batch": args.vit_batch}
-    for img in args.vit_img:
+    out = {"model": label, "batch": args.vit_batch}
+    for img in imgs:
         torch.manual_seed(2468 + img)
-        base = vit_tiny_patch16(img)
+        base = builder(img)
         elsa_fwd = copy.deepcopy(base)
         elsa_amd.patch_timm_attention(elsa_fwd)
         elsa_train = copy.deepcopy(base)
@@ -339,7 +350,7 @@ def _vit_bench(args, dt):
         models = {"sdpa": base.to("cuda", dt), "elsa": elsa_fwd.to("cuda", dt)}
         x = torch.randn(args.vit_batch, 3, img, img, device="cuda", dtype=dt)
         labels = torch.randint(0, 1000, (args.vit_batch,), device="cuda")
-        row = {"tokens": (img // 16) ** 2 + 1}
+        row = {"tokens": tokens(img)}
         for name, m in models.items():
             m.eval()
             row[f"{name}_fwd_ms"] = _graph_fwd_ms(m, x, args.vit_steps)
@@ -348,7 +359,7 @@ def _vit_bench(args, dt):
         for kind in ("fwd", "train"):
             row[f"elsa_{kind}_img_s"] = round(args.vit_batch / (row[f"elsa_{kind}_ms"] * 1e-3), 1)
             row[f"{kind}_lat_ratio_vs_sdpa"] = round(row[f"elsa_{kind}_ms"] / row[f"sdpa_{kind}_ms"], 3)
-        print(f"bench: vit_tiny {img}px {row}", file=sys.stderr, flush=True)
+        print(f"bench: {builder.__name__} {img}px {row}", file=sys.stderr, flush=True)
         out[str(img)] = row
         del models, elsa_train
         torch.cuda.empty_cache()

@@ -104,3 +104,37 @@ def test_hipgraph_capture_of_patched_forward_replays():
             eager = elsa(static_x)
         torch.cuda.synchronize()
         assert torch.equal(static_y, eager), i
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_hipgraph_capture_of_forward_and_backward(causal):
+    describe(f"hipgraph fwd+bwd causal={causal}")
+    shape = (1, 3, 1031, 64)
+    static = [torch.randn(shape, device="cuda", dtype=torch.float16) for _ in range(4)]
+    q, k, v, do = static
+
+    def run():
+        out, rm, rz = elsa_amd.twopass_attention_with_state(q, k, v, is_causal=causal)
+        return (out,) + tuple(elsa_amd.twopass_attention_backward(q, k, v, out, do, is_causal=causal, row_m=rm,
+                                                                   row_z=rz))
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = run()
+    g = torch.Generator(device="cuda").manual_seed(5)
+    for i in range(3):
+        for t in static:
+            t.copy_(torch.randn(shape, device="cuda", dtype=torch.float16, generator=g))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = run()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("out", "dq", "dk", "dv"), outs, eager):
+            assert torch.equal(a, b), (i, name)
