@@ -212,7 +212,9 @@ def _dense_bias_backward(
     dbias = torch.empty((bias_b, bias_h, seq_len, seq_len), dtype=torch.float32, device=q.device)
     args = _bwd_args(q_c, k_c, v_c, out_c, do_c, row_m.contiguous(), row_z.contiguous(), None, None, None, meta,
                      is_causal=is_causal, scale=scale)
-    ws = _attach_workspace(lib, args, q.device)
+    nbytes = int(lib.elsa_dbias_workspace_bytes(ctypes.byref(args), bias_b, bias_h))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
     with torch.cuda.device(q.device):
         _lib.check(lib.elsa_dbias(ctypes.byref(args), dbias.data_ptr(), bias_b, bias_h,
                                   _lib.stream_handle(q.device)), "elsa_dbias")

@@ -315,6 +315,17 @@ int elsa_row_stats(const elsa_bwd_args* a, float* row_m, float* row_z, void* str
   return ELSA_OK;
 }
 
+static size_t dbias_part_bytes(const elsa_bwd_args* a, int nsplit, int32_t bias_batch, int32_t bias_heads) {
+  if (nsplit <= 1) return 0;
+  return align256((size_t)nsplit * bias_batch * bias_heads * a->seq_len * a->seq_len * sizeof(float));
+}
+
+size_t elsa_dbias_workspace_bytes(const elsa_bwd_args* a, int32_t bias_batch, int32_t bias_heads) {
+  if (!a || a->batch <= 0 || a->heads <= 0 || a->seq_len <= 0 || bias_batch <= 0 || bias_heads <= 0) return 0;
+  const int ns = elsa::dbias_splits(a->seq_len, a->batch, a->heads, bias_batch, bias_heads);
+  return elsa_bwd_workspace_bytes(a) + dbias_part_bytes(a, ns, bias_batch, bias_heads);
+}
+
 int elsa_dbias(const elsa_bwd_args* a, float* dbias, int32_t bias_batch, int32_t bias_heads, void* stream) {
   int rc = check_bwd(a, false);
   if (rc) return rc;
@@ -327,7 +338,11 @@ int elsa_dbias(const elsa_bwd_args* a, float* dbias, int32_t bias_batch, int32_t
   if (!a->workspace || a->workspace_bytes < need)
     return fail(ELSA_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", a->workspace_bytes,
                 need);
-  hipError_t e = elsa::launch_dbias(bwd_params(a), dbias, bias_batch, bias_heads, a->dtype,
+  // split the reduction over broadcast (b, h) pairs when the workspace has room for the partials
+  int nsplit = elsa::dbias_splits(a->seq_len, a->batch, a->heads, bias_batch, bias_heads);
+  if (a->workspace_bytes < need + dbias_part_bytes(a, nsplit, bias_batch, bias_heads)) nsplit = 1;
+  float* part = nsplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(a->workspace) + need) : nullptr;
+  hipError_t e = elsa::launch_dbias(bwd_params(a), dbias, bias_batch, bias_heads, a->dtype, nsplit, part,
                                     static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "dbias launch");
   return ELSA_OK;

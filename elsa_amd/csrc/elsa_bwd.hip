@@ -12,6 +12,8 @@
 //
 // The same swap23 row permutation as the forward makes the D-layout registers of
 // S^T / S directly usable as the B operand of the following MFMA.
+#include <algorithm>
+
 #include "elsa_internal.h"
 #include "elsa_mfma.h"
 
@@ -773,22 +775,29 @@ __global__ __launch_bounds__(64 * WAVES) void row_stats_kernel(const BwdParams p
 // ------------------------------------------------------------------ dbias
 // One wave per 32x32 (row, key) tile of one (b', h'); operands straight from HBM.
 template <typename T, int DP>
-__global__ __launch_bounds__(64) void dbias_kernel(const BwdParams p, float* dbias, int bias_batch, int bias_heads) {
+// Grid: x = 32x32 output tile, y = bias head, z = bias batch x nsplit.  The sum over the
+// broadcast (b, h) pairs is cut into nsplit contiguous ranges; with nsplit > 1 each range
+// writes its partial tile to part[split] and dbias_reduce_kernel adds them in order.
+__global__ __launch_bounds__(64) void dbias_kernel(const BwdParams p, float* dbias, int bias_batch, int bias_heads,
+                                                   int nsplit, float* part) {
   using C = BwdCfg<T, DP>;
   using M = Mfma<T>;
   const int lane = threadIdx.x, c = lane & 31, g = lane >> 5;
   const int tiles = (p.N + 31) / 32;
   const int ti = blockIdx.x / tiles, tj = blockIdx.x % tiles;
-  const int hb = blockIdx.y, bb = blockIdx.z;
+  const int hb = blockIdx.y, bb = blockIdx.z / nsplit, split = blockIdx.z - bb * nsplit;
   const int my_row = ti * 32 + c;
   const int krow = tj * 32 + swap23(c);  // key loaded by this lane for the A operand
   const bool row_ok = my_row < p.N, krow_ok = krow < p.N;
   const int B = p.BH / p.H;
-  const int b_lo = bias_batch == 1 ? 0 : bb, b_hi = bias_batch == 1 ? B : bb + 1;
-  const int h_lo = bias_heads == 1 ? 0 : hb, h_hi = bias_heads == 1 ? p.H : hb + 1;
+  const int b_lo = bias_batch == 1 ? 0 : bb, nb = bias_batch == 1 ? B : 1;
+  const int h_lo = bias_heads == 1 ? 0 : hb, nh = bias_heads == 1 ? p.H : 1;
+  const int64_t pairs = (int64_t)nb * nh;
+  const int64_t r_lo = pairs * split / nsplit, r_hi = pairs * (split + 1) / nsplit;
   f32x16 acc = f32x16{};
-  for (int b = b_lo; b < b_hi; ++b)
-    for (int h = h_lo; h < h_hi; ++h) {
+  for (int64_t pair = r_lo; pair < r_hi; ++pair) {
+    {
+      const int b = b_lo + (int)(pair / nh), h = h_lo + (int)(pair % nh);
       const int bh = b * p.H + h;
       const int64_t hoff = (int64_t)bh * p.N * p.D;
       const T* Q = static_cast<const T*>(p.q) + hoff;
@@ -818,13 +827,24 @@ __global__ __launch_bounds__(64) void dbias_kernel(const BwdParams p, float* dbi
         acc[r] += pr * (dp[r] - dd);
       }
     }
+  }
   if (!row_ok) return;
-  float* outp = dbias + (((int64_t)bb * bias_heads + hb) * p.N + my_row) * p.N;
+  const int64_t plane = (int64_t)bias_batch * bias_heads * p.N * p.N;
+  float* outp = (nsplit == 1 ? dbias : part + split * plane) + (((int64_t)bb * bias_heads + hb) * p.N + my_row) * p.N;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int key = tj * 32 + key_of_reg(r, g);
     if (key < p.N) outp[key] = acc[r];
   }
+}
+
+// dbias = sum over split of part[split], in split order (deterministic).
+__global__ __launch_bounds__(256) void dbias_reduce_kernel(const float* part, float* dbias, int nsplit, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float acc = 0.f;
+  for (int sp = 0; sp < nsplit; ++sp) acc += part[sp * n + i];
+  dbias[i] = acc;
 }
 
 // ------------------------------------------------------------------ launchers
@@ -918,28 +938,43 @@ hipError_t launch_row_stats(const BwdParams& p, float* row_m, float* row_z, int 
 }
 
 template <typename T, int DP>
-static hipError_t db_launch2(const BwdParams& p, float* dbias, int bb, int hb, hipStream_t st) {
+static hipError_t db_launch2(const BwdParams& p, float* dbias, int bb, int hb, int nsplit, float* part,
+                             hipStream_t st) {
   hipError_t e = pre_launch<T>(p, st);
   if (e != hipSuccess) return e;
   const int tiles = (p.N + 31) / 32;
-  const dim3 grid(tiles * tiles, hb, bb);
-  hipLaunchKernelGGL((dbias_kernel<T, DP>), grid, dim3(64), 0, st, p, dbias, bb, hb);
+  const dim3 grid(tiles * tiles, hb, bb * nsplit);
+  hipLaunchKernelGGL((dbias_kernel<T, DP>), grid, dim3(64), 0, st, p, dbias, bb, hb, nsplit, part);
+  if ((e = hipGetLastError()) != hipSuccess || nsplit == 1) return e;
+  const int64_t n = (int64_t)bb * hb * p.N * p.N;
+  hipLaunchKernelGGL(dbias_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, dbias, nsplit, n);
   return hipGetLastError();
 }
 
 template <typename T>
-static hipError_t db_launch1(const BwdParams& p, float* dbias, int bb, int hb, hipStream_t st) {
+static hipError_t db_launch1(const BwdParams& p, float* dbias, int bb, int hb, int nsplit, float* part,
+                             hipStream_t st) {
   switch (pad_head_dim(p.D)) {
-    case 32: return db_launch2<T, 32>(p, dbias, bb, hb, st);
-    case 64: return db_launch2<T, 64>(p, dbias, bb, hb, st);
-    default: return db_launch2<T, 128>(p, dbias, bb, hb, st);
+    case 32: return db_launch2<T, 32>(p, dbias, bb, hb, nsplit, part, st);
+    case 64: return db_launch2<T, 64>(p, dbias, bb, hb, nsplit, part, st);
+    default: return db_launch2<T, 128>(p, dbias, bb, hb, nsplit, part, st);
   }
 }
 
-hipError_t launch_dbias(const BwdParams& p, float* dbias, int bias_batch, int bias_heads, int dtype, hipStream_t st) {
-  if (dtype == ELSA_F16) return db_launch1<f16>(p, dbias, bias_batch, bias_heads, st);
-  if (dtype == ELSA_BF16) return db_launch1<bf16>(p, dbias, bias_batch, bias_heads, st);
-  return db_launch1<float>(p, dbias, bias_batch, bias_heads, st);
+int dbias_splits(int N, int batch, int heads, int bias_batch, int bias_heads) {
+  const int64_t tiles = (N + 31) / 32;
+  const int64_t blocks = tiles * tiles * bias_batch * bias_heads;
+  const int64_t pairs = (int64_t)(bias_batch == 1 ? batch : 1) * (bias_heads == 1 ? heads : 1);
+  int64_t ns = (2048 + blocks - 1) / blocks;  // enough work-groups to fill 256 CUs several times
+  ns = std::min<int64_t>(ns, std::max<int64_t>(1, pairs / 4));  // at least 4 (b, h) pairs per split
+  return (int)std::max<int64_t>(1, std::min<int64_t>(ns, 256));
+}
+
+hipError_t launch_dbias(const BwdParams& p, float* dbias, int bias_batch, int bias_heads, int dtype, int nsplit,
+                        float* part, hipStream_t st) {
+  if (dtype == ELSA_F16) return db_launch1<f16>(p, dbias, bias_batch, bias_heads, nsplit, part, st);
+  if (dtype == ELSA_BF16) return db_launch1<bf16>(p, dbias, bias_batch, bias_heads, nsplit, part, st);
+  return db_launch1<float>(p, dbias, bias_batch, bias_heads, nsplit, part, st);
 }
 
 }  // namespace elsa

@@ -83,8 +83,11 @@ struct BwdParams {
 // stage < 0: preprocess, dq and dk/dv; 0: preprocess only; 1: dq only; 2: dk/dv only.
 hipError_t launch_bwd(const BwdParams& p, int dtype, int stage, hipStream_t stream);
 hipError_t launch_row_stats(const BwdParams& p, float* row_m, float* row_z, int dtype, hipStream_t stream);
-hipError_t launch_dbias(const BwdParams& p, float* dbias, int bias_batch, int bias_heads, int dtype,
-                        hipStream_t stream);
+// Number of ranges the dbias reduction over broadcast (b, h) pairs is cut into (1 = direct).
+int dbias_splits(int N, int batch, int heads, int bias_batch, int bias_heads);
+// part: nsplit * bias_batch * bias_heads * N * N floats of scratch when nsplit > 1.
+hipError_t launch_dbias(const BwdParams& p, float* dbias, int bias_batch, int bias_heads, int dtype, int nsplit,
+                        float* part, hipStream_t stream);
 hipError_t launch_debug_mfma(int variant, const void* a, const void* b, float* d, hipStream_t stream);
 
 }  // namespace elsa

@@ -141,9 +141,16 @@ int elsa_bwd_stage(const elsa_bwd_args* args, int32_t stage, void* stream);
 /* Recompute the base-2 row state (row_m, row_z) from q, k (and bias). Uses
  * args->q, k, bias, shape fields; writes row_m/row_z [B*H, N]. */
 int elsa_row_stats(const elsa_bwd_args* args, float* row_m, float* row_z, void* stream);
+/* Workspace for elsa_dbias: elsa_bwd_workspace_bytes plus room for the partial sums of a
+ * reduction split over the broadcast (b, h) pairs.  No counterpart in the reference (its
+ * dbias kernel loops over the broadcast dims in one program per tile,
+ * attention_bwd.py:529-624); like elsa_bwd_workspace_bytes it lets the caller allocate. */
+size_t elsa_dbias_workspace_bytes(const elsa_bwd_args* args, int32_t bias_batch, int32_t bias_heads);
 /* dbias[b', h', i, j] = sum over broadcast (b, h) of p*(dp - D), fp32 output of
  * shape [bias_batch, bias_heads, N, N] (bias_batch in {1,B}, bias_heads in {1,H}).
- * Needs args->row_m/row_z and the bias descriptor. */
+ * Needs args->row_m/row_z and the bias descriptor.  With a workspace of
+ * elsa_dbias_workspace_bytes the reduction is split across work-groups and summed in a
+ * fixed order (deterministic); with only elsa_bwd_workspace_bytes it runs unsplit. */
 int elsa_dbias(const elsa_bwd_args* args, float* dbias, int32_t bias_batch, int32_t bias_heads,
                void* stream);
 

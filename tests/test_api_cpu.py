@@ -110,6 +110,8 @@ def test_bwd_and_dbias_reject_bad_args_without_launching():
     b.out = b.dout = b.dq = b.dk = b.dv = b.row_m = b.row_z = 1
     assert lib.elsa_bwd(ctypes.byref(b), None) == _lib.ELSA_ERR_WORKSPACE
     assert lib.elsa_bwd_workspace_bytes(ctypes.byref(b)) >= 2 * 64 * 4
+    assert lib.elsa_dbias_workspace_bytes(ctypes.byref(b), 1, 1) >= lib.elsa_bwd_workspace_bytes(ctypes.byref(b))
+    assert lib.elsa_dbias_workspace_bytes(ctypes.byref(b), 0, 1) == 0
     assert lib.elsa_dbias(ctypes.byref(b), 1, 2, 1, None) == _lib.ELSA_ERR_INVALID  # bias_batch 2 vs B=1
     assert lib.elsa_debug_mfma(5, 1, 1, 1, None) == _lib.ELSA_ERR_INVALID
 

@@ -135,3 +135,41 @@ def test_dbias_causal_matches_closed_form():
     eo, em, ez = O.exact_forward(q, k, v, bias=bias, is_causal=True)
     edb = O.dbias(q, k, v, eo, do, em, ez, bias=bias, is_causal=True)
     assert max_abs(host(db), edb) <= 1e-6
+
+
+@pytest.mark.parametrize("bias_shape", [(1, 3, 49, 49), (49, 49)])
+def test_dbias_split_reduction_matches_unsplit_and_closed_form(bias_shape):
+    """Swin-like shape (many windows folded into each bias entry): the reduction over the
+    broadcast (b, h) pairs is split across work-groups and summed in order."""
+    import ctypes
+
+    from elsa_amd import _lib
+    from elsa_amd.attention import _canonical_bias
+    from elsa_amd.attention_bwd import _bwd_args
+
+    describe(f"dbias split {bias_shape}")
+    shape = (64, 3, 49, 32)
+    q, k, v, do = O.make_inputs(shape, seed=21, dtype="fp32", with_dout=True, dout_scale=0.1)
+    bias = (np.random.default_rng(21).standard_normal(bias_shape) * 0.5).astype(np.float32)
+    qd, kd, vd, dod, bd = (dev(x, "fp32") for x in (q, k, v, do, bias))
+    out, rm, rz = elsa_amd.twopass_attention_with_state(qd, kd, vd, bias=bd)
+    split = _dense_bias_backward(qd, kd, vd, out, dod, bias=bd, is_causal=False, row_m=rm, row_z=rz)
+    eo, em, ez = O.exact_forward(q, k, v, bias=bias)
+    edb = O.dbias(q, k, v, eo, do, em, ez, bias=bias)
+    assert max_abs(host(split), edb) <= 1e-6 * (shape[0] * shape[1]) ** 0.5
+
+    # the same call with only the backward workspace runs unsplit
+    lib = _lib.load()
+    meta = _canonical_bias(bd, batch=shape[0], heads=shape[1], seq_len=shape[2], device=qd.device)
+    bias_b = 1 if meta.stride_b == 0 else shape[0]
+    bias_h = 1 if meta.stride_h == 0 else shape[1]
+    args = _bwd_args(qd, kd, vd, out, dod, rm, rz, None, None, None, meta, is_causal=False, scale=1 / np.sqrt(32))
+    small = int(lib.elsa_bwd_workspace_bytes(ctypes.byref(args)))
+    assert int(lib.elsa_dbias_workspace_bytes(ctypes.byref(args), bias_b, bias_h)) > small
+    ws = torch.empty(small, dtype=torch.uint8, device=qd.device)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), small
+    unsplit = torch.empty((bias_b, bias_h, 49, 49), dtype=torch.float32, device=qd.device)
+    _lib.check(lib.elsa_dbias(ctypes.byref(args), unsplit.data_ptr(), bias_b, bias_h, _lib.stream_handle(qd.device)),
+               "elsa_dbias")
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(host(split).reshape(-1), host(unsplit).reshape(-1), rtol=1e-5, atol=1e-6)
