@@ -127,11 +127,17 @@ FwdBuffers carve(const elsa_fwd_args* a, const elsa_fwd_plan& pl) {
   return b;
 }
 
+// which: 1 = Phase 1 (summaries), 2 = Phase 2, 3 = Phase 1 with Phase 2's finalize fused
+// into its epilogue (only for a single partition, where the merge is the identity)
 int run_phase(const elsa_fwd_args* a, const elsa_fwd_plan& pl, int q_start, int q_len, hipStream_t st, int which) {
   FwdBuffers wb = carve(a, pl);
   const int bh = a->batch * a->heads;
-  if (which == 1) {
+  if (which == 1 || which == 3) {
     elsa::Phase1Params p{};
+    p.direct = which == 3 ? 1 : 0;
+    p.out = a->out;
+    p.row_m = a->row_m;
+    p.row_z = a->row_z;
     p.q = a->q;
     p.k = a->k;
     p.v = a->v;
@@ -263,6 +269,10 @@ int elsa_fwd(const elsa_fwd_args* a, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   for (int q0 = 0; q0 < a->seq_len; q0 += pl.q_chunk) {
     const int len = std::min(pl.q_chunk, a->seq_len - q0);
+    if (pl.partitions == 1) {
+      if ((rc = run_phase(a, pl, q0, len, st, 3))) return rc;
+      continue;
+    }
     if ((rc = run_phase(a, pl, q0, len, st, 1))) return rc;
     if ((rc = run_phase(a, pl, q0, len, st, 2))) return rc;
   }

@@ -77,6 +77,39 @@ __device__ inline void store4(void* base, int64_t off, int dtype, float a, float
   }
 }
 
+// Epilogue of one row of one partition: the summary (m, z, s) for Phase 2, or, when the
+// partition is the whole row (p.direct), Phase 2's finalize in place: s rounded to the
+// summary dtype as the summary store would round it, out = s / z (0 when z == 0), and the
+// row state (m, z) -- the values Phase 2 computes for a single partition.
+__device__ inline float round_to(int dtype, float x) {
+  if (dtype == ELSA_F16) return static_cast<float>(static_cast<f16>(x));
+  if (dtype == ELSA_BF16) return static_cast<float>(static_cast<bf16>(x));
+  return x;
+}
+__device__ inline void emit_state(const Phase1Params& p, int64_t ridx, int64_t orow, float m, float z) {
+  if (!p.direct) {
+    p.m_buf[ridx] = m;
+    p.z_buf[ridx] = z;
+  } else if (p.row_m != nullptr) {
+    p.row_m[orow] = z > 0.f ? m : kNegInf;
+    p.row_z[orow] = z;
+  }
+}
+template <typename T>
+__device__ inline void emit4(const Phase1Params& p, int64_t ridx, int64_t orow, int d, float z, float a, float b,
+                             float c, float e) {
+  if (!p.direct) {
+    store4(p.s_buf, ridx * p.D + d, p.s_dtype, a, b, c, e);
+    return;
+  }
+  typedef T t4 __attribute__((ext_vector_type(4)));
+  const float v[4] = {a, b, c, e};
+  t4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = static_cast<T>(z > 0.f ? round_to(p.s_dtype, v[i]) / z : 0.f);
+  *reinterpret_cast<t4*>(static_cast<T*>(p.out) + orow * p.D + d) = o;
+}
+
 template <typename T, int DP, int WAVES, bool HAS_BIAS>
 __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p) {
   using C = FwdCfg<T, DP>;
@@ -272,18 +305,16 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
   const float z = wave_sum_pair(z_lane);
   if (!row_ok) return;
   const int64_t ridx = ((int64_t)kb * p.BH + bh) * p.rows_pad + (my_row - p.q_start);
-  if (g == 0) {
-    p.m_buf[ridx] = m_run;
-    p.z_buf[ridx] = z;
-  }
+  const int64_t orow = (int64_t)bh * p.N + my_row;
+  if (g == 0) emit_state(p, ridx, orow, m_run, z);
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int d = dt * 32 + q4 * 8 + 4 * g;
       if (d < p.D)
-        store4(p.s_buf, ridx * p.D + d, p.s_dtype, oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
-               oacc[dt][4 * q4 + 3]);
+        emit4<T>(p, ridx, orow, d, z, oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
+                 oacc[dt][4 * q4 + 3]);
     }
 }
 
@@ -533,18 +564,17 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     // renormalise to the exact row maximum (m_run <= m_true <= m_run + kLazyTau)
     const float f = (m_true[rt] == kNegInf) ? 1.f : fast_exp2(m_run[rt] - m_true[rt]);
     const int64_t ridx = ((int64_t)kb * p.BH + bh) * p.rows_pad + (my_row - p.q_start);
-    if (g == 0) {
-      p.m_buf[ridx] = m_true[rt];
-      p.z_buf[ridx] = z_raw * f;
-    }
+    const int64_t orow = (int64_t)bh * p.N + my_row;
+    const float z = z_raw * f;
+    if (g == 0) emit_state(p, ridx, orow, m_true[rt], z);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int d = dt * 32 + q4 * 8 + 4 * g;
         if (d < p.D)
-          store4(p.s_buf, ridx * p.D + d, p.s_dtype, oacc[rt][dt][4 * q4] * f, oacc[rt][dt][4 * q4 + 1] * f,
-                 oacc[rt][dt][4 * q4 + 2] * f, oacc[rt][dt][4 * q4 + 3] * f);
+          emit4<T>(p, ridx, orow, d, z, oacc[rt][dt][4 * q4] * f, oacc[rt][dt][4 * q4 + 1] * f,
+                   oacc[rt][dt][4 * q4 + 2] * f, oacc[rt][dt][4 * q4 + 3] * f);
       }
   }
 }

@@ -35,6 +35,12 @@ struct Phase1Params {
   float scale_log2;  // log2(e) / sqrt(D_model)
   float bias_log2;   // log2(e)
   int64_t rows_pad;
+  // direct != 0 (only with P == 1): apply Phase 2's finalize in the epilogue and write
+  // out [B*H, N, D] (the input dtype) and the row state instead of the summary
+  int direct;
+  void* out;
+  float* row_m;
+  float* row_z;
 };
 
 struct Phase2Params {

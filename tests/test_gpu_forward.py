@@ -201,3 +201,29 @@ def test_north_star_shape_properties():
     assert max_abs(host(out)[:, :, rows], eo) <= 1e-3
     assert max_abs(host(out), host(out8)) <= 1e-3
     assert max_abs(host(out), host(outp)) <= 1e-3
+
+
+@pytest.mark.parametrize("shape,dt,causal,bias", [((8, 3, 197, 64), "fp16", False, False),
+                                                  ((2, 2, 300, 128), "bf16", True, False),
+                                                  ((4, 3, 49, 32), "fp32", False, True)])
+def test_single_partition_fused_finalize_matches_two_launches(shape, dt, causal, bias):
+    """With one K partition the forward applies Phase 2's finalize inside Phase 1; the result
+    must equal, bit for bit, the explicit Phase 1 + Phase 2 launches on the same plan."""
+    describe(f"fused finalize {shape} {dt} causal={causal} bias={bias}")
+    q, k, v = O.make_inputs(shape, seed=31, dtype=dt)
+    qd, kd, vd = dev(q, dt), dev(k, dt), dev(v, dt)
+    plan = forward_plan(qd, is_causal=causal)
+    assert plan["partitions"] == 1
+    if bias:
+        b = dev((np.random.default_rng(31).standard_normal((shape[1], shape[2], shape[2])) * 0.5)
+                .astype(np.float32), "fp32")
+        out, rm, rz = elsa_amd.twopass_attention_with_state(qd, kd, vd, bias=b, is_causal=causal)
+        o2, m2, z2 = elsa_amd.twopass_attention_with_state(qd, kd, vd, bias=b, is_causal=causal,
+                                                           q_chunk_size=shape[2] // 2 + 1)
+        assert torch.equal(out, o2) and torch.equal(rm, m2) and torch.equal(rz, z2)
+        return
+    out, rm, rz = elsa_amd.twopass_attention_with_state(qd, kd, vd, is_causal=causal)
+    o2, m2, z2, *_ = two_pass_explicit(qd, kd, vd, is_causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(out, o2)
+    assert torch.equal(rm, m2) and torch.equal(rz, z2)
