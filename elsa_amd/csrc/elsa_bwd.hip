@@ -507,8 +507,10 @@ static_for<0, NCH>([&](auto I) {
   }
 }
 
+// 2 waves per SIMD up to D = 64; at D = 128 the dK/dV accumulators and the wave's K/V
+// fragments alone need more than the 256 registers of that budget, so 1 wave per SIMD
 template <typename T, int DP, int KRT, int WAVES, bool HAS_BIAS>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(DP >= 128 ? 1 : 2, 2)))
 void bwd_dkdv_half_kernel(const BwdParams p) {
   using M = Mfma<T>;
   typedef typename M::frag F;

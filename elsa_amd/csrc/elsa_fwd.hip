@@ -126,7 +126,7 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31, g = lane >> 5;
-  const WgCoord wg = xcd_order();
+  const WgCoord wg = phase1_order(p.causal);
   const int bh = wg.y, kb = wg.z;
   const int q_end = p.q_start + p.q_len;
   const int wg_row0 = p.q_start + wg.x * BM;
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31, g = lane >> 5;
-  const WgCoord wg = xcd_order();
+  const WgCoord wg = phase1_order(p.causal);
   const int bh = wg.y, kb = wg.z;
   const int q_end = p.q_start + p.q_len;
   const int wg_row0 = p.q_start + wg.x * BM;

@@ -168,13 +168,27 @@ __device__ inline i16x4 lds_read_tr16(const void* p) {
 struct WgCoord {
   int x, y, z;
 };
-__device__ inline WgCoord xcd_order() {
-  const int gx = gridDim.x, gy = gridDim.y;
-  const int n = gx * gy * gridDim.z;
-  const int lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+__device__ inline int xcd_linear() {
+  const int n = gridDim.x * gridDim.y * gridDim.z;
+  const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
   const int per = n >> 3, rem = n & 7, xcd = lin & 7, slot = lin >> 3;
-  const int l = xcd * per + min(xcd, rem) + slot;
+  return xcd * per + min(xcd, rem) + slot;
+}
+__device__ inline WgCoord xcd_order() {
+  const int gx = gridDim.x, gy = gridDim.y, l = xcd_linear();
   return {l % gx, (l / gx) % gy, l / (gx * gy)};
+}
+// Phase 1 order (grid x = row block, y = head, z = K partition).  Non-causal: the XCD
+// order with z varying fastest, so one XCD's range covers all partitions of consecutive
+// row blocks of one head and the row block's Q tile is shared in L2 by its partitions.
+// Causal: the work of a row block grows with its index and vanishes for partitions past
+// it; there the dispatcher's own round-robin over XCDs balances best, with the row blocks
+// reversed so that the heaviest start first.
+__device__ inline WgCoord phase1_order(bool causal) {
+  const int gx = gridDim.x, gz = gridDim.z;
+  if (causal) return {gx - 1 - (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
+  const int l = xcd_linear(), rest = l / gz;
+  return {rest % gx, rest / gx, l % gz};
 }
 
 // Combine the two 32-lane halves of a wave (lanes l and l ^ 32) with
