@@ -51,6 +51,19 @@ class BiasDesc(ctypes.Structure):
     ]
 
 
+class Layout(ctypes.Structure):
+    """elsa_layout: element strides (batch, head, row) of a [B,H,N,D] operand; zeros = dense."""
+
+    _fields_ = [("batch", c_int64), ("head", c_int64), ("row", c_int64)]
+
+
+def layout_of(t) -> "Layout":
+    """Strides of a [B,H,N,D] tensor with a contiguous last dim, as an elsa_layout."""
+    sb, sh, sn, sd = t.stride()
+    assert sd == 1
+    return Layout(sb, sh, sn)
+
+
 class FwdArgs(ctypes.Structure):
     _fields_ = [
         ("q", c_void_p),
@@ -72,6 +85,10 @@ class FwdArgs(ctypes.Structure):
         ("scale", c_float),
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
+        ("q_layout", Layout),
+        ("k_layout", Layout),
+        ("v_layout", Layout),
+        ("out_layout", Layout),
     ]
 
 
@@ -113,7 +130,8 @@ class BwdArgs(ctypes.Structure):
     ]
 
 
-_STRUCTS = {0: FwdArgs, 1: FwdPlan, 2: BwdArgs, 3: BiasDesc}
+_STRUCTS = {0: FwdArgs, 1: FwdPlan, 2: BwdArgs, 3: BiasDesc, 4: Layout}
+ABI_VERSION = 2
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -147,8 +165,8 @@ def load() -> ctypes.CDLL:
     for fn in ("elsa_fwd_plan_get", "elsa_fwd", "elsa_phase1", "elsa_phase2", "elsa_bwd", "elsa_bwd_stage", "elsa_row_stats",
                "elsa_dbias", "elsa_debug_mfma"):
         getattr(lib, fn).restype = c_int32
-    if lib.elsa_abi_version() != 1:
-        raise RuntimeError(f"{LIB_PATH}: ABI version {lib.elsa_abi_version()} != 1")
+    if lib.elsa_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH}: ABI version {lib.elsa_abi_version()} != {ABI_VERSION}")
     for which, st in _STRUCTS.items():
         if lib.elsa_struct_size(which) != ctypes.sizeof(st):
             raise RuntimeError(f"{LIB_PATH}: struct {st.__name__} size mismatch "

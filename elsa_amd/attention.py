@@ -160,6 +160,17 @@ def _resolve_precision(input_precision: str, dtype: torch.dtype) -> str:
     return input_precision
 
 
+def _operand(x: torch.Tensor) -> torch.Tensor:
+    """x itself when the kernels can read it in place (contiguous head dim of a multiple of
+    8 elements, batch/head/row strides that are multiples of 8, 16-byte aligned base),
+    else a dense, padded copy."""
+    st = x.stride()
+    if (x.shape[-1] % 8 == 0 and st[-1] == 1 and all(s % 8 == 0 and s >= 0 for s in st[:3])
+            and st[2] >= x.shape[-1] and x.data_ptr() % 16 == 0):
+        return x
+    return _pad_head_dim(x.contiguous())
+
+
 def _pad_head_dim(x: torch.Tensor) -> torch.Tensor:
     """Zero-pad the head dim to a multiple of 8 and make the base 16-byte aligned.
 
@@ -189,6 +200,8 @@ def _make_fwd_args(q_c, k_c, v_c, out, row_m, row_z, bias_meta: _BiasMeta, *, is
     a.partition_len = int(partition_len or 0)
     a.q_chunk = int(q_chunk or 0)
     a.scale = float(scale)
+    a.q_layout, a.k_layout, a.v_layout = (_lib.layout_of(t) for t in (q_c, k_c, v_c))
+    a.out_layout = _lib.layout_of(out)
     return a
 
 
@@ -203,15 +216,25 @@ def _elsa_forward(
     partition_len: Optional[int],
     q_chunk: Optional[int],
     want_state: bool,
+    out_bnhd: bool = False,
 ):
-    """Run Phase 1 + Phase 2 on the HIP library.  Returns (out, row_m, row_z, q_c, k_c, v_c)."""
+    """Run Phase 1 + Phase 2 on the HIP library.  Returns (out, row_m, row_z, q_c, k_c, v_c).
+
+    q, k, v may be strided views (read in place when ``_operand`` allows); ``out_bnhd``
+    allocates the output as [B, N, H, D] memory (returned as its [B, H, N, D] view), so
+    that ``out.transpose(1, 2).reshape(B, N, H * D)`` costs no copy.
+    """
     lib = _lib.load()
     batch, heads, seq_len, head_dim = map(int, q.shape)
-    q_c, k_c, v_c = q.contiguous(), k.contiguous(), v.contiguous()
     bias_meta = _canonical_bias(bias, batch=batch, heads=heads, seq_len=seq_len, device=q.device)
     scale = 1.0 / math.sqrt(head_dim)
-    qp, kp, vp = _pad_head_dim(q_c), _pad_head_dim(k_c), _pad_head_dim(v_c)
-    out = torch.empty(qp.shape, dtype=q.dtype, device=q.device)
+    qp, kp, vp = _operand(q), _operand(k), _operand(v)
+    q_c, k_c, v_c = qp, kp, vp
+    dp = int(qp.shape[-1])
+    if out_bnhd and dp == head_dim:
+        out = torch.empty((batch, seq_len, heads, dp), dtype=q.dtype, device=q.device).permute(0, 2, 1, 3)
+    else:
+        out = torch.empty((batch, heads, seq_len, dp), dtype=q.dtype, device=q.device)
     row_m = torch.empty((batch * heads, seq_len), device=q.device, dtype=torch.float32) if want_state else None
     row_z = torch.empty_like(row_m) if want_state else None
     args = _make_fwd_args(qp, kp, vp, out, row_m, row_z, bias_meta, is_causal=is_causal,
@@ -223,8 +246,9 @@ def _elsa_forward(
     args.workspace_bytes = int(plan.workspace_bytes)
     with torch.cuda.device(q.device):
         _lib.check(lib.elsa_fwd(ctypes.byref(args), _lib.stream_handle(q.device)), "elsa_fwd")
-    if qp.shape[-1] != head_dim:
+    if dp != head_dim:
         out = out[..., :head_dim].contiguous()
+        q_c, k_c, v_c = (t[..., :head_dim] for t in (qp, kp, vp))
     return out, row_m, row_z, q_c, k_c, v_c
 
 
@@ -267,8 +291,20 @@ def twopass_attention(
     """Strict two-pass ELSA attention (reference attention.py:239-321).
 
     Phase 1 writes one exact ``(m, z, s)`` summary per K partition; Phase 2 merges
-    the partition summaries of every row and emits ``s / z``.
+    the partition summaries of every row and emits ``s / z``.  q, k and v may be strided
+    views (e.g. slices of a fused qkv projection): they are read in place when their
+    strides allow.
     """
+    return _twopass_attention(q, k, v, bias=bias, is_causal=is_causal, block_m=block_m, block_n=block_n,
+                              q_chunk_size=q_chunk_size, summary_dtype=summary_dtype, phase1_warps=phase1_warps,
+                              phase2_warps=phase2_warps, phase1_stages=phase1_stages, phase2_stages=phase2_stages,
+                              input_precision=input_precision, algorithm=algorithm, out_bnhd=False)
+
+
+def _twopass_attention(q, k, v, *, bias, is_causal, block_m, block_n, q_chunk_size, summary_dtype, phase1_warps,
+                       phase2_warps, phase1_stages, phase2_stages, input_precision, algorithm, out_bnhd):
+    """twopass_attention; ``out_bnhd`` returns a [B,H,N,D] view of [B,N,H,D] memory (for
+    callers that go on to ``transpose(1, 2).reshape(B, N, H*D)``, which is then free)."""
     _check_qkv(q, k, v, "twopass_attention")
     if algorithm not in ("auto", "paper_scan"):
         raise ValueError("only algorithm='paper_scan' is available in this strict release")
@@ -285,7 +321,7 @@ def twopass_attention(
     if batch * heads == 0:
         return torch.empty_like(q)
     out, *_ = _elsa_forward(q, k, v, bias=bias, is_causal=is_causal, summary_dtype=sdt, partition_len=part,
-                            q_chunk=qc, want_state=False)
+                            q_chunk=qc, want_state=False, out_bnhd=out_bnhd)
     return out
 
 

@@ -71,7 +71,7 @@ def twopass_attention_with_state(
         q, k, v, bias=bias, is_causal=is_causal, summary_dtype=sdt, partition_len=part, q_chunk=qc, want_state=True
     )
     if return_contiguous_inputs:
-        return out, row_m, row_z, q_c, k_c, v_c
+        return out, row_m, row_z, q_c.contiguous(), k_c.contiguous(), v_c.contiguous()
     return out, row_m, row_z
 
 

@@ -3,10 +3,12 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <string>
 
 #include "elsa_hip.h"
+
 #include "elsa_internal.h"
 
 namespace {
@@ -127,6 +129,19 @@ FwdBuffers carve(const elsa_fwd_args* a, const elsa_fwd_plan& pl) {
   return b;
 }
 
+// Element strides (batch, head, row) of a [B,H,N,D] operand; an all-zero layout is dense.
+void resolve_layout(const elsa_layout& l, int H, int N, int D, int64_t out[3]) {
+  if (l.batch == 0 && l.head == 0 && l.row == 0) {
+    out[0] = (int64_t)H * N * D;
+    out[1] = (int64_t)N * D;
+    out[2] = D;
+  } else {
+    out[0] = l.batch;
+    out[1] = l.head;
+    out[2] = l.row;
+  }
+}
+
 // which: 1 = Phase 1 (summaries), 2 = Phase 2, 3 = Phase 1 with Phase 2's finalize fused
 // into its epilogue (only for a single partition, where the merge is the identity)
 int run_phase(const elsa_fwd_args* a, const elsa_fwd_plan& pl, int q_start, int q_len, hipStream_t st, int which) {
@@ -138,6 +153,10 @@ int run_phase(const elsa_fwd_args* a, const elsa_fwd_plan& pl, int q_start, int 
     p.out = a->out;
     p.row_m = a->row_m;
     p.row_z = a->row_z;
+    resolve_layout(a->q_layout, a->heads, a->seq_len, a->head_dim, p.qs);
+    resolve_layout(a->k_layout, a->heads, a->seq_len, a->head_dim, p.ks);
+    resolve_layout(a->v_layout, a->heads, a->seq_len, a->head_dim, p.vs);
+    resolve_layout(a->out_layout, a->heads, a->seq_len, a->head_dim, p.os);
     p.q = a->q;
     p.k = a->k;
     p.v = a->v;
@@ -179,9 +198,27 @@ int run_phase(const elsa_fwd_args* a, const elsa_fwd_plan& pl, int q_start, int 
     p.P = pl.partitions;
     p.causal = a->is_causal ? 1 : 0;
     p.rows_pad = pl.q_chunk;
+    p.H = a->heads;
+    resolve_layout(a->out_layout, a->heads, a->seq_len, a->head_dim, p.os);
     hipError_t e = elsa::launch_phase2(p, st);
     if (e != hipSuccess) return hip_fail(e, "phase2 launch");
   }
+  return ELSA_OK;
+}
+
+int check_layout(const char* name, const void* ptr, const elsa_layout& l, const elsa_fwd_args* a,
+                 int64_t part_len) {
+  int64_t s[3];
+  resolve_layout(l, a->heads, a->seq_len, a->head_dim, s);
+  if (s[0] < 0 || s[1] < 0 || s[2] < a->head_dim)
+    return fail(ELSA_ERR_INVALID, "%s layout (%lld, %lld, %lld) needs non-negative strides and a row stride >= "
+                "head_dim", name, (long long)s[0], (long long)s[1], (long long)s[2]);
+  if ((s[0] | s[1] | s[2]) % 8 != 0 || reinterpret_cast<uintptr_t>(ptr) % 16 != 0)
+    return fail(ELSA_ERR_INVALID, "%s: strides must be multiples of 8 elements and the pointer 16-byte aligned",
+                name);
+  if (part_len * s[2] * (int64_t)dtype_size(a->dtype) >= (int64_t(1) << 31))
+    return fail(ELSA_ERR_UNSUPPORTED, "%s: a K partition spans >= 2 GiB (partition_len %lld x row stride %lld)",
+                name, (long long)part_len, (long long)s[2]);
   return ELSA_OK;
 }
 
@@ -192,6 +229,11 @@ int check_fwd_call(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
   if (!a->workspace || a->workspace_bytes < pl->workspace_bytes)
     return fail(ELSA_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", a->workspace_bytes,
                 pl->workspace_bytes);
+  if ((rc = check_layout("q", a->q, a->q_layout, a, pl->partition_len)) ||
+      (rc = check_layout("k", a->k, a->k_layout, a, pl->partition_len)) ||
+      (rc = check_layout("v", a->v, a->v_layout, a, pl->partition_len)) ||
+      (rc = check_layout("out", a->out, a->out_layout, a, pl->partition_len)))
+    return rc;
   return ELSA_OK;
 }
 
@@ -256,6 +298,7 @@ size_t elsa_struct_size(int which) {
     case 1: return sizeof(elsa_fwd_plan);
     case 2: return sizeof(elsa_bwd_args);
     case 3: return sizeof(elsa_bias_desc);
+    case 4: return sizeof(elsa_layout);
     default: return 0;
   }
 }

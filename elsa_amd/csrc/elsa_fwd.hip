@@ -96,7 +96,7 @@ __device__ inline void emit_state(const Phase1Params& p, int64_t ridx, int64_t o
   }
 }
 template <typename T>
-__device__ inline void emit4(const Phase1Params& p, int64_t ridx, int64_t orow, int d, float z, float a, float b,
+__device__ inline void emit4(const Phase1Params& p, int64_t ridx, int64_t ooff, int d, float z, float a, float b,
                              float c, float e) {
   if (!p.direct) {
     store4(p.s_buf, ridx * p.D + d, p.s_dtype, a, b, c, e);
@@ -107,7 +107,7 @@ __device__ inline void emit4(const Phase1Params& p, int64_t ridx, int64_t orow, 
   t4 o;
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = static_cast<T>(z > 0.f ? round_to(p.s_dtype, v[i]) / z : 0.f);
-  *reinterpret_cast<t4*>(static_cast<T*>(p.out) + orow * p.D + d) = o;
+  *reinterpret_cast<t4*>(static_cast<T*>(p.out) + ooff + d) = o;
 }
 
 template <typename T, int DP, int WAVES, bool HAS_BIAS>
@@ -139,18 +139,17 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
   const int row0 = wg_row0 + wave * 32;
   const int my_row = row0 + c;
   const bool row_ok = my_row < q_end;
-  const int64_t hoff = (int64_t)bh * p.N * p.D;
-  const T* __restrict__ Q = static_cast<const T*>(p.q) + hoff;
-  const T* __restrict__ K = static_cast<const T*>(p.k) + hoff;
-  const T* __restrict__ V = static_cast<const T*>(p.v) + hoff;
   const int bi = bh / p.H, hi = bh - (bh / p.H) * p.H;
+  const T* __restrict__ Q = static_cast<const T*>(p.q) + bi * p.qs[0] + hi * p.qs[1];
+  const T* __restrict__ K = static_cast<const T*>(p.k) + bi * p.ks[0] + hi * p.ks[1];
+  const T* __restrict__ V = static_cast<const T*>(p.v) + bi * p.vs[0] + hi * p.vs[1];
 
   // Q^T fragments (B operand of S^T = K Q^T): lane (c, g) holds Q[row c][d = kk*KSTEP + g*KP + t].
   F qf[C::NKK];
 #pragma unroll
   for (int kk = 0; kk < C::NKK; ++kk) {
     const int d0 = kk * C::KSTEP + g * C::KP;
-    qf[kk] = load_frag<T>(Q + (int64_t)(row_ok ? my_row : 0) * p.D + d0, row_ok && d0 < p.D);
+    qf[kk] = load_frag<T>(Q + (int64_t)(row_ok ? my_row : 0) * p.qs[2] + d0, row_ok && d0 < p.D);
   }
 
   Chunk16 kreg[NCH], vreg[NCH];
@@ -161,9 +160,8 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
       const int key = ci / CPR, d0 = (ci % CPR) * C::CE;
       const int ka = t0 + key;
       if (ka < k_end && d0 < p.D) {
-        const int64_t off = (int64_t)ka * p.D + d0;
-        kreg[i] = *reinterpret_cast<const Chunk16*>(K + off);
-        vreg[i] = *reinterpret_cast<const Chunk16*>(V + off);
+        kreg[i] = *reinterpret_cast<const Chunk16*>(K + (int64_t)ka * p.ks[2] + d0);
+        vreg[i] = *reinterpret_cast<const Chunk16*>(V + (int64_t)ka * p.vs[2] + d0);
       } else {
         kreg[i] = Chunk16{};
         vreg[i] = Chunk16{};
@@ -306,6 +304,7 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
   if (!row_ok) return;
   const int64_t ridx = ((int64_t)kb * p.BH + bh) * p.rows_pad + (my_row - p.q_start);
   const int64_t orow = (int64_t)bh * p.N + my_row;
+  const int64_t ooff = bi * p.os[0] + hi * p.os[1] + (int64_t)my_row * p.os[2];
   if (g == 0) emit_state(p, ridx, orow, m_run, z);
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt)
@@ -313,7 +312,7 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
     for (int q4 = 0; q4 < 4; ++q4) {
       const int d = dt * 32 + q4 * 8 + 4 * g;
       if (d < p.D)
-        emit4<T>(p, ridx, orow, d, z, oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
+        emit4<T>(p, ridx, ooff, d, z, oacc[dt][4 * q4], oacc[dt][4 * q4 + 1], oacc[dt][4 * q4 + 2],
                  oacc[dt][4 * q4 + 3]);
     }
 }
@@ -360,11 +359,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   if (k_begin >= k_end) return;  // every row of this workgroup sees the identity here
 
   const int row0 = wg_row0 + wave * ROWS_W;
-  const int64_t hoff = (int64_t)bh * p.N * p.D;
-  const T* __restrict__ Q = static_cast<const T*>(p.q) + hoff;
-  const T* __restrict__ K = static_cast<const T*>(p.k) + hoff;
-  const T* __restrict__ V = static_cast<const T*>(p.v) + hoff;
   const int bi = bh / p.H, hi = bh - (bh / p.H) * p.H;
+  const T* __restrict__ Q = static_cast<const T*>(p.q) + bi * p.qs[0] + hi * p.qs[1];
+  const T* __restrict__ K = static_cast<const T*>(p.k) + bi * p.ks[0] + hi * p.ks[1];
+  const T* __restrict__ V = static_cast<const T*>(p.v) + bi * p.vs[0] + hi * p.vs[1];
 
   F qf[RT][NKK];
 #pragma unroll
@@ -374,7 +372,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
     for (int kk = 0; kk < NKK; ++kk) {
       const int d0 = kk * 16 + g * 8;
-      qf[rt][kk] = load_frag<T>(Q + (int64_t)(ok ? row : 0) * p.D + d0, ok && d0 < p.D);
+      qf[rt][kk] = load_frag<T>(Q + (int64_t)(ok ? row : 0) * p.qs[2] + d0, ok && d0 < p.D);
     }
   }
 
@@ -384,23 +382,27 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 
   // K/V of this partition through buffer resources: keys past k_end and head-dim
   // padding (d0 >= D) read as zeros
-  const uint32_t part_bytes = (uint32_t)(k_end - k_begin) * (uint32_t)p.D * (uint32_t)sizeof(T);
-  const auto rk = make_rsrc(K + (int64_t)k_begin * p.D, part_bytes);
-  const auto rv = make_rsrc(V + (int64_t)k_begin * p.D, part_bytes);
-  uint32_t voff[NCH];
+  // (row strides below 2^31 / part_len bytes: checked by the planner)
+  const uint32_t krs = (uint32_t)p.ks[2] * (uint32_t)sizeof(T), vrs = (uint32_t)p.vs[2] * (uint32_t)sizeof(T);
+  const auto rk = make_rsrc(K + (int64_t)k_begin * p.ks[2], (uint32_t)(k_end - k_begin) * krs);
+  const auto rv = make_rsrc(V + (int64_t)k_begin * p.vs[2], (uint32_t)(k_end - k_begin) * vrs);
+  uint32_t kvoff[NCH], vvoff[NCH];
   static_for<0, NCH>([&](auto I) {
     constexpr int i = decltype(I)::value;
     const int ci = tid + i * NT;
     const int key = ci / CPR, d0 = (ci % CPR) * 8;
-    voff[i] = d0 < p.D ? (uint32_t)(key * p.D + d0) * (uint32_t)sizeof(T) : kBufferOff;
+    const uint32_t dofs = (uint32_t)d0 * (uint32_t)sizeof(T);
+    kvoff[i] = d0 < p.D ? (uint32_t)key * krs + dofs : kBufferOff;
+    vvoff[i] = d0 < p.D ? (uint32_t)key * vrs + dofs : kBufferOff;
   });
   Chunk16 kreg[NCH], vreg[NCH];
   auto gload = [&](int t0) {
-    const uint32_t soff = (uint32_t)(t0 - k_begin) * (uint32_t)p.D * (uint32_t)sizeof(T);
+    // the stage offset goes into the VGPR offset, so that the range check sees it
+    const uint32_t kt = (uint32_t)(t0 - k_begin);
     static_for<0, NCH>([&](auto I) {
       constexpr int i = decltype(I)::value;
-      kreg[i] = buffer_load16(rk, voff[i], soff);
-      vreg[i] = buffer_load16(rv, voff[i], soff);
+      kreg[i] = buffer_load16(rk, kvoff[i] + kt * krs, 0);
+      vreg[i] = buffer_load16(rv, vvoff[i] + kt * vrs, 0);
     });
   };
   auto sstore = [&](int buf) {
@@ -565,6 +567,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     const float f = (m_true[rt] == kNegInf) ? 1.f : fast_exp2(m_run[rt] - m_true[rt]);
     const int64_t ridx = ((int64_t)kb * p.BH + bh) * p.rows_pad + (my_row - p.q_start);
     const int64_t orow = (int64_t)bh * p.N + my_row;
+    const int64_t ooff = bi * p.os[0] + hi * p.os[1] + (int64_t)my_row * p.os[2];
     const float z = z_raw * f;
     if (g == 0) emit_state(p, ridx, orow, m_true[rt], z);
 #pragma unroll
@@ -573,7 +576,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
       for (int q4 = 0; q4 < 4; ++q4) {
         const int d = dt * 32 + q4 * 8 + 4 * g;
         if (d < p.D)
-          emit4<T>(p, ridx, orow, d, z, oacc[rt][dt][4 * q4] * f, oacc[rt][dt][4 * q4 + 1] * f,
+          emit4<T>(p, ridx, ooff, d, z, oacc[rt][dt][4 * q4] * f, oacc[rt][dt][4 * q4 + 1] * f,
                    oacc[rt][dt][4 * q4 + 2] * f, oacc[rt][dt][4 * q4 + 3] * f);
       }
   }
@@ -658,7 +661,8 @@ __global__ __launch_bounds__(256) void phase2_kernel(const Phase2Params p) {
     mono_merge(am, az, as, m[0], z[0], s[0], am, az, as);
   }
 
-  TO* out = static_cast<TO*>(p.out) + ((int64_t)bh * p.N + row) * p.D + ch * 8;
+  const int bi = bh / p.H, hi = bh - bi * p.H;
+  TO* out = static_cast<TO*>(p.out) + bi * p.os[0] + hi * p.os[1] + (int64_t)row * p.os[2] + ch * 8;
   typedef TO o8 __attribute__((ext_vector_type(8)));
   o8 ov;
 #pragma unroll

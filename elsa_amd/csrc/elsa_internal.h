@@ -36,11 +36,13 @@ struct Phase1Params {
   float bias_log2;   // log2(e)
   int64_t rows_pad;
   // direct != 0 (only with P == 1): apply Phase 2's finalize in the epilogue and write
-  // out [B*H, N, D] (the input dtype) and the row state instead of the summary
+  // out (the input dtype, layout os) and the row state instead of the summary
   int direct;
   void* out;
   float* row_m;
   float* row_z;
+  // element strides (batch, head, row) of q, k, v and out; the head dim is contiguous
+  int64_t qs[3], ks[3], vs[3], os[3];
 };
 
 struct Phase2Params {
@@ -57,6 +59,8 @@ struct Phase2Params {
   int part_len, P;
   int causal;
   int64_t rows_pad;
+  int H;
+  int64_t os[3];  // element strides (batch, head, row) of out
 };
 
 // Launch helpers (return hipError_t of the launch).

@@ -128,10 +128,10 @@ __device__ inline void static_for(Fn&& f) {
 // LDS by memcpy is not split into registers (it ends up in LDS or scratch).
 typedef uint32_t Chunk16 __attribute__((ext_vector_type(4)));
 
-// Raw buffer resource over [base, base + bytes): loads at offsets >= bytes return
-// zeros, which is the key-range masking the tile loaders need, with no per-chunk
-// address arithmetic or compare in VGPRs.  bytes must stay below 2^31 so that an
-// offset pushed past it by kBufferOff never wraps.
+// Raw buffer resource over [base, base + bytes): loads whose VGPR offset is >= bytes
+// return zeros (callers keep the SGPR offset at 0 so that the whole offset is
+// range-checked), which is the key-range masking the tile loaders need without compares.
+// bytes must stay below 2^31 so that an offset pushed past it by kBufferOff never wraps.
 constexpr uint32_t kBufferOff = 0x80000000u;
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);

@@ -17,7 +17,7 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from .attention import twopass_attention
+from .attention import _twopass_attention
 from .vision_models import relative_position_index, resize_rel_pos_bias_table
 
 
@@ -46,10 +46,21 @@ def _vit_state(module: nn.Module, source: nn.Module, elsa_kwargs: Optional[dict]
 
 def _vit_qkv(module: nn.Module, x: torch.Tensor):
     batch, seq_len, _ = x.shape
-    # one contiguous [3, B, H, N, D] tensor so the unbound q/k/v need no further copies
+    # strided [B, H, N, D] views of the fused projection: the kernels read them in place
     qkv = module.qkv(x).reshape(batch, seq_len, 3, module.num_heads, module.head_dim).permute(2, 0, 3, 1, 4)
-    q, k, v = qkv.contiguous().unbind(0)
+    q, k, v = qkv.unbind(0)
     return module.q_norm(q), module.k_norm(k), v
+
+
+def _attend(q, k, v, kwargs, bias=None):
+    """twopass_attention with the output laid out as [B, N, H, D] (free transpose after)."""
+    kw = dict(bias=None, is_causal=False, block_m=None, block_n=None, q_chunk_size=None, summary_dtype=None,
+              phase1_warps=None, phase2_warps=None, phase1_stages=None, phase2_stages=None, input_precision="auto",
+              algorithm="auto")
+    kw.update(kwargs)
+    if bias is not None:
+        kw["bias"] = bias
+    return _twopass_attention(q, k, v, out_bnhd=True, **kw)
 
 
 def _vit_out(module: nn.Module, y: torch.Tensor, batch: int, seq_len: int) -> torch.Tensor:
@@ -66,7 +77,7 @@ class ElsaTimmVitAttention(nn.Module):
         if attn_mask is not None:
             raise ValueError("ELSA ViT drop-in currently supports unmasked attention only")
         q, k, v = _vit_qkv(self, x)
-        y = twopass_attention(q, k, v, **self.elsa_kwargs)
+        y = _attend(q, k, v, self.elsa_kwargs)
         return _vit_out(self, y, x.shape[0], x.shape[1])
 
 
@@ -150,7 +161,7 @@ class ElsaTimmSwinWindowAttention(_SwinWindowCommon):
         if self.training and self.attn_drop.p:
             raise ValueError("ELSA Swin drop-in forward is inference-only when attention dropout is nonzero")
         q, k, v, bias = self._qkv_and_bias(x, mask)
-        y = twopass_attention(q, k, v, bias=bias, **self._elsa_kwargs_for_window(x.shape[1]))
+        y = _attend(q, k, v, self._elsa_kwargs_for_window(x.shape[1]), bias=bias)
         return self._out(y, x.shape[0], x.shape[1])
 
 

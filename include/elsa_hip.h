@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define ELSA_ABI_VERSION 1
+#define ELSA_ABI_VERSION 2
 
 typedef enum elsa_dtype { ELSA_F16 = 0, ELSA_BF16 = 1, ELSA_F32 = 2 } elsa_dtype;
 
@@ -69,6 +69,15 @@ typedef struct elsa_bias_desc {
   int64_t stride_b, stride_h, stride_q, stride_k;
 } elsa_bias_desc;
 
+/* Element strides of a [B, H, N, D] operand whose last dimension is contiguous.
+ * All zero means the dense layout (H*N*D, N*D, D).  Non-dense layouts let callers hand
+ * over views without a copy, e.g. q/k/v sliced out of a fused [B, N, 3, H, D] projection
+ * or an output written straight into [B, N, H, D].  Row strides must be multiples of 8
+ * elements and base pointers 16-byte aligned. */
+typedef struct elsa_layout {
+  int64_t batch, head, row;
+} elsa_layout;
+
 typedef struct elsa_fwd_args {
   const void* q;
   const void* k;
@@ -86,6 +95,7 @@ typedef struct elsa_fwd_args {
   float scale;           /* softmax scale on q.k; 0 = 1/sqrt(head_dim)          */
   void* workspace;
   size_t workspace_bytes;
+  elsa_layout q_layout, k_layout, v_layout, out_layout; /* zero = dense [B,H,N,D]  */
 } elsa_fwd_args;
 
 typedef struct elsa_fwd_plan {
@@ -122,7 +132,7 @@ typedef struct elsa_bwd_args {
 int elsa_abi_version(void);
 const char* elsa_last_error(void);
 /* sizeof of the argument structs as compiled into the library (ABI check). */
-size_t elsa_struct_size(int which); /* 0 fwd_args, 1 fwd_plan, 2 bwd_args, 3 bias_desc */
+size_t elsa_struct_size(int which); /* 0 fwd_args, 1 fwd_plan, 2 bwd_args, 3 bias_desc, 4 layout */
 
 /* Tiling, partition routing and workspace size for a forward call. */
 int elsa_fwd_plan_get(const elsa_fwd_args* args, elsa_fwd_plan* plan);

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_struct_sizes():
     lib = _lib.load()
-    assert lib.elsa_abi_version() == 1
+    assert lib.elsa_abi_version() == _lib.ABI_VERSION == 2
     for which, st in _lib._STRUCTS.items():
         assert lib.elsa_struct_size(which) == ctypes.sizeof(st)
 

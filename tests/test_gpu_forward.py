@@ -16,7 +16,7 @@ import torch
 import elsa_amd
 from elsa_amd.attention import forward_plan, two_pass_explicit
 from oracle import elsa_oracle as O
-from tests.gpu_util import FWD_TOL, assert_parity, describe, dev, host, max_abs
+from tests.gpu_util import FWD_TOL, TORCH_DT, assert_parity, describe, dev, host, max_abs
 
 pytestmark = pytest.mark.gpu
 
@@ -227,3 +227,33 @@ def test_single_partition_fused_finalize_matches_two_launches(shape, dt, causal,
     torch.cuda.synchronize()
     assert torch.equal(out, o2)
     assert torch.equal(rm, m2) and torch.equal(rz, z2)
+
+
+@pytest.mark.parametrize("dt,n,causal", [("fp16", 197, False), ("bf16", 4097, True), ("fp32", 300, False),
+                                         ("fp16", 16384, False)])
+def test_strided_operands_read_in_place(dt, n, causal):
+    """q/k/v as views of a fused [B, N, 3, H, D] projection (and a head-broadcast k) and an
+    output written as [B, N, H, D] memory give the same bits as dense operands."""
+    from elsa_amd.attention import _twopass_attention
+
+    describe(f"strided {dt} n={n} causal={causal}")
+    b, h, d = 2, 3, 64
+    g = torch.Generator().manual_seed(n)
+    qkv = torch.randn((b, n, 3, h, d), generator=g).to(TORCH_DT[dt]).cuda()
+    q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+    assert not q.is_contiguous()
+    dense = elsa_amd.twopass_attention(q.contiguous(), k.contiguous(), v.contiguous(), is_causal=causal)
+    strided = elsa_amd.twopass_attention(q, k, v, is_causal=causal)
+    kw = dict(bias=None, is_causal=causal, block_m=None, block_n=None, q_chunk_size=None, summary_dtype=None,
+              phase1_warps=None, phase2_warps=None, phase1_stages=None, phase2_stages=None,
+              input_precision="auto", algorithm="auto")
+    bnhd = _twopass_attention(q, k, v, out_bnhd=True, **kw)
+    assert bnhd.transpose(1, 2).is_contiguous()
+    torch.cuda.synchronize()
+    assert torch.equal(strided, dense) and torch.equal(bnhd, dense)
+    # a key/value shared by all heads (stride 0 over heads)
+    k1 = k[:, :1].expand(b, h, n, d)
+    v1 = v[:, :1].expand(b, h, n, d)
+    shared = elsa_amd.twopass_attention(q, k1, v1, is_causal=causal)
+    ref = elsa_amd.twopass_attention(q.contiguous(), k1.contiguous(), v1.contiguous(), is_causal=causal)
+    assert torch.equal(shared, ref)
