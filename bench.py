@@ -43,6 +43,9 @@ def _args():
     ap.add_argument("--dtype", choices=["fp16", "bf16", "fp32"], default="fp16")
     ap.add_argument("--causal", action="store_true")
     ap.add_argument("--block-n", type=int, default=None, help="K-partition width (default: planner)")
+    ap.add_argument("--fill", choices=["randn", "sign", "zeros", "const"], default="randn",
+                    help="input values: N(0,1) (the benchmark), their signs, zeros or 0.5 everywhere; the "
+                         "kernels run the same instructions for all four, which isolates the data-dependent clock")
     ap.add_argument("--cpu-baseline", dest="cpu_baseline", action="store_true", default=True)
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
     ap.add_argument("--cpu-rows", type=int, default=1536, help="query rows of the CPU-baseline sample")
@@ -145,7 +148,15 @@ def main() -> int:
     B, H, N, D = args.batch, args.heads, args.seq, args.dim
     shape = (B, H, N, D)
     g = torch.Generator().manual_seed(2026)
-    q, k, v, do = (torch.randn(shape, generator=g).to(dt).to(dev) for _ in range(4))
+    def _input():
+        x = torch.randn(shape, generator=g)
+        if args.fill == "sign":
+            x = x.sign()
+        elif args.fill != "randn":
+            x = torch.full(shape, 0.0 if args.fill == "zeros" else 0.5)
+        return x.to(dt).to(dev)
+
+    q, k, v, do = (_input() for _ in range(4))
     causal = bool(args.causal)
     print(f"bench: {shape} {args.dtype} causal={causal} steps={args.steps} warmup={args.warmup}", file=sys.stderr,
           flush=True)
@@ -280,7 +291,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": args.dtype,
-        "data": "synthetic: q,k,v,dO ~ N(0,1), torch.Generator seed 2026, resident in HBM",
+        "data": ("synthetic: q,k,v,dO ~ N(0,1), torch.Generator seed 2026, resident in HBM" if args.fill == "randn"
+                 else f"synthetic, diagnostic fill '{args.fill}' (not the benchmark input)"),
         "config": {"workload": "ELSA two-pass attention fwd(with row state)+bwd, "
                                + ("causal" if causal else "non-causal"),
                    "batch": B, "heads": H, "seq_len": N, "head_dim": D,
