@@ -76,6 +76,18 @@ def test_plan_partitions_cover_sequence(n, bh, d):
     assert p.q_chunk >= 1
 
 
+@pytest.mark.parametrize("n,parts", [(8192, 2), (16384, 4), (32768, 8), (65536, 16)])
+def test_plan_causal_uses_4096_key_partitions_from_8k(n, parts):
+    rc, p = _plan(_args(n=n, causal=1))
+    assert rc == 0 and p.partition_len == 4096 and p.partitions == parts
+
+
+def test_plan_causal_short_sequences_keep_the_workgroup_target():
+    rc_c, pc = _plan(_args(n=2048, causal=1))
+    rc_n, pn = _plan(_args(n=2048))
+    assert rc_c == rc_n == 0 and pc.partition_len == pn.partition_len == 512
+
+
 def test_plan_user_partition_and_chunk():
     rc, p = _plan(_args(n=513, bh=(1, 2), part=128, qc=128))
     assert rc == 0 and p.partition_len == 128 and p.partitions == 5 and p.q_chunk == 128
