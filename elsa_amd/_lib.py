@@ -127,11 +127,19 @@ class BwdArgs(ctypes.Structure):
         ("_pad", c_int32),
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
+        ("q_layout", Layout),
+        ("k_layout", Layout),
+        ("v_layout", Layout),
+        ("out_layout", Layout),
+        ("dout_layout", Layout),
+        ("dq_layout", Layout),
+        ("dk_layout", Layout),
+        ("dv_layout", Layout),
     ]
 
 
 _STRUCTS = {0: FwdArgs, 1: FwdPlan, 2: BwdArgs, 3: BiasDesc, 4: Layout}
-ABI_VERSION = 2
+ABI_VERSION = 3
 _lib: Optional[ctypes.CDLL] = None
 
 

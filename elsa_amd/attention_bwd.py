@@ -23,7 +23,7 @@ from .attention import (
     _canonical_bias,
     _check_qkv,
     _elsa_forward,
-    _pad_head_dim,
+    _operand,
     _resolve_forward_options,
     _resolve_precision,
     _validate_warps,
@@ -50,6 +50,17 @@ def twopass_attention_with_state(
     return_contiguous_inputs: bool = False,
 ) -> tuple[torch.Tensor, ...]:
     """Training forward: ``(out, row_m, row_z[, q_c, k_c, v_c])`` with base-2 row state."""
+    return _with_state(q, k, v, bias=bias, is_causal=is_causal, block_m=block_m, block_n=block_n,
+                       q_chunk_size=q_chunk_size, summary_dtype=summary_dtype, phase1_warps=phase1_warps,
+                       phase2_warps=phase2_warps, phase1_stages=phase1_stages, phase2_stages=phase2_stages,
+                       input_precision=input_precision, algorithm=algorithm,
+                       return_contiguous_inputs=return_contiguous_inputs, out_bnhd=False)
+
+
+def _with_state(q, k, v, *, bias=None, is_causal=False, block_m=None, block_n=None, q_chunk_size=None,
+                summary_dtype=None, phase1_warps=None, phase2_warps=None, phase1_stages=None, phase2_stages=None,
+                input_precision="auto", algorithm="auto", return_contiguous_inputs=False, out_bnhd=False):
+    """twopass_attention_with_state; ``out_bnhd`` returns out as a [B,H,N,D] view of [B,N,H,D] memory."""
     _check_qkv(q, k, v, "twopass_attention_with_state")
     batch, heads, seq_len, head_dim = map(int, q.shape)
     if seq_len <= 0:
@@ -68,7 +79,8 @@ def twopass_attention_with_state(
         phase2_stages=phase2_stages, input_precision=input_precision,
     )
     out, row_m, row_z, q_c, k_c, v_c = _elsa_forward(
-        q, k, v, bias=bias, is_causal=is_causal, summary_dtype=sdt, partition_len=part, q_chunk=qc, want_state=True
+        q, k, v, bias=bias, is_causal=is_causal, summary_dtype=sdt, partition_len=part, q_chunk=qc, want_state=True,
+        out_bnhd=out_bnhd,
     )
     if return_contiguous_inputs:
         return out, row_m, row_z, q_c.contiguous(), k_c.contiguous(), v_c.contiguous()
@@ -76,12 +88,18 @@ def twopass_attention_with_state(
 
 
 def _bwd_args(q_c, k_c, v_c, out_c, do_c, row_m, row_z, dq, dk, dv, bias_meta, *, is_causal, scale):
+    """elsa_bwd_args for [B,H,N,D] tensors, which may be strided views (their layouts are passed)."""
     batch, heads, seq_len, head_dim = map(int, q_c.shape)
     a = _lib.BwdArgs()
     a.q, a.k, a.v = q_c.data_ptr(), k_c.data_ptr(), v_c.data_ptr()
     a.out, a.dout = _lib.ptr(out_c), _lib.ptr(do_c)
     a.row_m, a.row_z = _lib.ptr(row_m), _lib.ptr(row_z)
     a.dq, a.dk, a.dv = _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv)
+    a.q_layout, a.k_layout, a.v_layout = (_lib.layout_of(t) for t in (q_c, k_c, v_c))
+    if out_c is not None:
+        a.out_layout, a.dout_layout = _lib.layout_of(out_c), _lib.layout_of(do_c)
+    if dq is not None:
+        a.dq_layout, a.dk_layout, a.dv_layout = (_lib.layout_of(t) for t in (dq, dk, dv))
     a.bias = _lib.bias_desc(bias_meta.tensor, (bias_meta.stride_b, bias_meta.stride_h, bias_meta.stride_q,
                                                bias_meta.stride_k))
     a.batch, a.heads, a.seq_len, a.head_dim = batch, heads, seq_len, head_dim
@@ -154,29 +172,43 @@ def twopass_attention_backward(
         if t.dtype != q.dtype:
             raise ValueError("q, k, v, out, and grad_out must share one dtype")
     bh = batch * heads
-    scale = 1.0 / math.sqrt(head_dim)
-    lib = _lib.load()
-    q_c, k_c, v_c = (_pad_head_dim(t.contiguous()) for t in (q, k, v))
-    out_c, do_c = (_pad_head_dim(t.contiguous()) for t in (out, grad_out))
     bias_meta = _canonical_bias(bias, batch=batch, heads=heads, seq_len=seq_len, device=q.device)
-    if row_m is None or row_z is None:
-        row_m, row_z = _row_stats(q_c, k_c, bias_meta, is_causal=is_causal, scale=scale)
-    else:
+    if row_m is not None and row_z is not None:
         if row_m.shape != (bh, seq_len) or row_z.shape != (bh, seq_len):
             raise ValueError("row_m and row_z must have shape [B*H,N]")
         row_m = row_m.contiguous().float()
         row_z = row_z.contiguous().float()
-    dq = torch.empty_like(q_c)
-    dk = torch.empty_like(k_c)
-    dv = torch.empty_like(v_c)
+    return _backward(q, k, v, out, grad_out, bias_meta, is_causal=is_causal, row_m=row_m, row_z=row_z)
+
+
+def _backward(q, k, v, out, grad_out, bias_meta, *, is_causal, row_m, row_z, grads=None):
+    """dq, dk, dv on the HIP library.  Operands are read in place when their layout allows
+    (``_operand``); ``grads`` optionally names [B,H,N,D] (possibly strided) tensors to write
+    dq, dk, dv into, such as views of one fused qkv gradient."""
+    head_dim = int(q.shape[-1])
+    scale = 1.0 / math.sqrt(head_dim)
+    lib = _lib.load()
+    q_c, k_c, v_c, out_c, do_c = (_operand(t) for t in (q, k, v, out, grad_out))
+    if row_m is None or row_z is None:
+        row_m, row_z = _row_stats(q_c, k_c, bias_meta, is_causal=is_causal, scale=scale)
+    padded = q_c.shape[-1] != head_dim
+    if grads is None or padded:
+        dq, dk, dv = (torch.empty(t.shape, dtype=t.dtype, device=t.device) for t in (q_c, k_c, v_c))
+    else:
+        dq, dk, dv = grads
     args = _bwd_args(q_c, k_c, v_c, out_c, do_c, row_m, row_z, dq, dk, dv, bias_meta, is_causal=is_causal,
                      scale=scale)
     ws = _attach_workspace(lib, args, q.device)
     with torch.cuda.device(q.device):
         _lib.check(lib.elsa_bwd(ctypes.byref(args), _lib.stream_handle(q.device)), "elsa_bwd")
     del ws
-    if q_c.shape[-1] != head_dim:
-        dq, dk, dv = (t[..., :head_dim].contiguous() for t in (dq, dk, dv))
+    if padded:
+        dq, dk, dv = (t[..., :head_dim] for t in (dq, dk, dv))
+        if grads is not None:
+            for dst, src in zip(grads, (dq, dk, dv)):
+                dst.copy_(src)
+            return grads
+        dq, dk, dv = (t.contiguous() for t in (dq, dk, dv))
     return dq, dk, dv
 
 
@@ -205,8 +237,7 @@ def _dense_bias_backward(
     bias_b = 1 if meta.stride_b == 0 else batch
     bias_h = 1 if meta.stride_h == 0 else heads
     scale = 1.0 / math.sqrt(head_dim)
-    q_c, k_c, v_c = (_pad_head_dim(t.contiguous()) for t in (q, k, v))
-    out_c, do_c = (_pad_head_dim(t.contiguous()) for t in (out, grad_out))
+    q_c, k_c, v_c, out_c, do_c = (_operand(t) for t in (q, k, v, out, grad_out))
     if row_m is None or row_z is None:
         row_m, row_z = _row_stats(q_c, k_c, meta, is_causal=is_causal, scale=scale)
     dbias = torch.empty((bias_b, bias_h, seq_len, seq_len), dtype=torch.float32, device=q.device)
@@ -223,36 +254,122 @@ def _dense_bias_backward(
 
 
 class _TwopassAttentionAutograd(torch.autograd.Function):
+    """Forward with row state, recompute backward (reference attention_bwd.py:842-905).
+
+    The reference saves contiguous copies of q, k, v; here the inputs are saved as given
+    and the backward kernels read them in place whenever their layout allows."""
+
     @staticmethod
-    def forward(ctx, q, k, v, bias, is_causal, fwd_kwargs, bwd_kwargs):
-        out, row_m, row_z, q_saved, k_saved, v_saved = twopass_attention_with_state(
-            q, k, v, bias=bias, is_causal=is_causal, return_contiguous_inputs=True, **fwd_kwargs
-        )
-        if bias is None:
-            saved_bias = torch.empty(1, device=q.device, dtype=torch.float32)
-            has_bias = False
-        else:
-            saved_bias = bias
-            has_bias = True
-        ctx.save_for_backward(q_saved, k_saved, v_saved, out, saved_bias, row_m, row_z)
-        ctx.has_bias = has_bias
-        ctx.bias_requires_grad = bool(bias is not None and bias.requires_grad)
-        ctx.is_causal = bool(is_causal)
-        ctx.bwd_kwargs = dict(bwd_kwargs)
+    def forward(ctx, q, k, v, bias, is_causal, fwd_kwargs, bwd_kwargs, out_bnhd=False):
+        out, row_m, row_z = _with_state(q, k, v, bias=bias, is_causal=is_causal, out_bnhd=out_bnhd, **fwd_kwargs)
+        _save(ctx, (q, k, v), out, bias, row_m, row_z, is_causal, bwd_kwargs)
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        q, k, v, out, saved_bias, row_m, row_z = ctx.saved_tensors
-        bias = saved_bias if ctx.has_bias else None
+        q, k, v, out, bias, row_m, row_z = _saved(ctx)
         dq, dk, dv = twopass_attention_backward(
             q, k, v, out, grad_out, bias=bias, is_causal=ctx.is_causal, row_m=row_m, row_z=row_z, **ctx.bwd_kwargs
         )
-        dbias = None
-        if ctx.bias_requires_grad:
-            dbias = _dense_bias_backward(q, k, v, out, grad_out, bias=bias, is_causal=ctx.is_causal, row_m=row_m,
-                                         row_z=row_z)
-        return dq, dk, dv, dbias, None, None, None
+        return dq, dk, dv, _dbias(ctx, q, k, v, out, grad_out, bias, row_m, row_z), None, None, None, None
+
+
+class _TwopassQkvAutograd(torch.autograd.Function):
+    """The same on a fused [B, N, 3, H, D] qkv projection (the timm drop-ins' layout).
+
+    q, k, v are read as strided views of it, out is written as [B, N, H, D] memory, and
+    the backward writes dq, dk, dv straight into one [B, N, 3, H, D] gradient, so neither
+    pass makes a transposing copy."""
+
+    @staticmethod
+    def forward(ctx, qkv, bias, is_causal, fwd_kwargs, bwd_kwargs):
+        q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+        out, row_m, row_z = _with_state(q, k, v, bias=bias, is_causal=is_causal, out_bnhd=True, **fwd_kwargs)
+        _save(ctx, (qkv,), out, bias, row_m, row_z, is_causal, bwd_kwargs)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        qkv, out, bias, row_m, row_z = _saved(ctx)
+        q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+        batch, heads, seq_len, _ = map(int, q.shape)
+        dqkv = torch.empty_like(qkv, memory_format=torch.contiguous_format)
+        grads = dqkv.permute(2, 0, 3, 1, 4).unbind(0)
+        meta = _canonical_bias(bias, batch=batch, heads=heads, seq_len=seq_len, device=q.device)
+        _backward(q, k, v, out, grad_out, meta, is_causal=ctx.is_causal, row_m=row_m, row_z=row_z, grads=grads)
+        return dqkv, _dbias(ctx, q, k, v, out, grad_out, bias, row_m, row_z), None, None, None
+
+
+def _save(ctx, inputs, out, bias, row_m, row_z, is_causal, bwd_kwargs):
+    ctx.has_bias = bias is not None
+    saved_bias = bias if bias is not None else torch.empty(0, device=out.device)
+    ctx.save_for_backward(*inputs, out, saved_bias, row_m, row_z)
+    ctx.bias_requires_grad = bool(bias is not None and bias.requires_grad)
+    ctx.is_causal = bool(is_causal)
+    ctx.bwd_kwargs = dict(bwd_kwargs)
+
+
+def _saved(ctx):
+    *inputs, out, saved_bias, row_m, row_z = ctx.saved_tensors
+    return (*inputs, out, saved_bias if ctx.has_bias else None, row_m, row_z)
+
+
+def _dbias(ctx, q, k, v, out, grad_out, bias, row_m, row_z):
+    if not ctx.bias_requires_grad:
+        return None
+    return _dense_bias_backward(q, k, v, out, grad_out, bias=bias, is_causal=ctx.is_causal, row_m=row_m, row_z=row_z)
+
+
+def _split_train_kwargs(bwd_block_m, bwd_block_n, bwd_num_warps, bwd_num_stages, bwd_input_precision, fwd_kwargs):
+    if bwd_input_precision == "auto":
+        fwd_input_precision = fwd_kwargs.get("input_precision")
+        if fwd_input_precision in ("ieee", "tf32", "tf32x3"):
+            bwd_input_precision = fwd_input_precision
+    bwd_kwargs = {
+        "block_m": bwd_block_m,
+        "block_n": bwd_block_n,
+        "num_warps": bwd_num_warps,
+        "num_stages": bwd_num_stages,
+        "input_precision": bwd_input_precision,
+    }
+    return {key: value for key, value in bwd_kwargs.items() if value is not None}
+
+
+def qkv_attention_train(qkv: torch.Tensor, *, bias: Optional[torch.Tensor] = None, is_causal: bool = False,
+                        bwd_block_m: Optional[int] = None, bwd_block_n: Optional[int] = None,
+                        bwd_num_warps: Optional[int] = None, bwd_num_stages: Optional[int] = None,
+                        bwd_input_precision: Literal["auto", "ieee", "tf32", "tf32x3"] = "auto",
+                        **fwd_kwargs) -> torch.Tensor:
+    """``twopass_attention_train`` on q, k, v = ``qkv[:, :, 0..2]`` of a [B, N, 3, H, D] tensor.
+
+    Returns the [B, H, N, D] output as a view of [B, N, H, D] memory; the gradient of qkv
+    comes back in qkv's own layout.  Same numerics as ``twopass_attention_train``."""
+    if qkv.dim() != 5 or qkv.shape[2] != 3:
+        raise ValueError("qkv must have shape [B,N,3,H,D]")
+    bwd_kwargs = _split_train_kwargs(bwd_block_m, bwd_block_n, bwd_num_warps, bwd_num_stages, bwd_input_precision,
+                                     fwd_kwargs)
+    _check_bwd_kwargs(bwd_kwargs, qkv.dtype)
+    return _TwopassQkvAutograd.apply(qkv, bias, is_causal, dict(fwd_kwargs), bwd_kwargs)
+
+
+def _check_bwd_kwargs(bwd_kwargs, dtype):
+    """The validation twopass_attention_backward applies to its tile knobs (attention_bwd.py:698-716)."""
+    _resolve_precision(bwd_kwargs.get("input_precision", "auto"), dtype)
+    for key in ("block_m", "block_n"):
+        if bwd_kwargs.get(key) is not None:
+            max(16, int(bwd_kwargs[key]))
+    if bwd_kwargs.get("num_warps") is not None:
+        _validate_warps("num_warps", bwd_kwargs["num_warps"])
+    if bwd_kwargs.get("num_stages") is not None:
+        max(1, int(bwd_kwargs["num_stages"]))
+
+
+def _train_bnhd(q, k, v, *, bias=None, is_causal=False, bwd_block_m=None, bwd_block_n=None, bwd_num_warps=None,
+                bwd_num_stages=None, bwd_input_precision="auto", **fwd_kwargs):
+    """twopass_attention_train with out returned as a [B,H,N,D] view of [B,N,H,D] memory."""
+    bwd_kwargs = _split_train_kwargs(bwd_block_m, bwd_block_n, bwd_num_warps, bwd_num_stages, bwd_input_precision,
+                                     fwd_kwargs)
+    return _TwopassAttentionAutograd.apply(q, k, v, bias, is_causal, dict(fwd_kwargs), bwd_kwargs, True)
 
 
 def twopass_attention_train(
@@ -270,16 +387,6 @@ def twopass_attention_train(
     **fwd_kwargs,
 ) -> torch.Tensor:
     """Autograd wrapper: two-pass forward with state plus recompute backward (attention_bwd.py:1003-1030)."""
-    if bwd_input_precision == "auto":
-        fwd_input_precision = fwd_kwargs.get("input_precision")
-        if fwd_input_precision in ("ieee", "tf32", "tf32x3"):
-            bwd_input_precision = fwd_input_precision
-    bwd_kwargs = {
-        "block_m": bwd_block_m,
-        "block_n": bwd_block_n,
-        "num_warps": bwd_num_warps,
-        "num_stages": bwd_num_stages,
-        "input_precision": bwd_input_precision,
-    }
-    bwd_kwargs = {key: value for key, value in bwd_kwargs.items() if value is not None}
+    bwd_kwargs = _split_train_kwargs(bwd_block_m, bwd_block_n, bwd_num_warps, bwd_num_stages, bwd_input_precision,
+                                     fwd_kwargs)
     return _TwopassAttentionAutograd.apply(q, k, v, bias, is_causal, dict(fwd_kwargs), bwd_kwargs)

@@ -211,16 +211,29 @@ int run_phase(const elsa_fwd_args* a, const elsa_fwd_plan& pl, int q_start, int 
   return ELSA_OK;
 }
 
-int check_layout(const char* name, const void* ptr, const elsa_layout& l, const elsa_fwd_args* a,
-                 int64_t part_len) {
-  int64_t s[3];
-  resolve_layout(l, a->heads, a->seq_len, a->head_dim, s);
-  if (s[0] < 0 || s[1] < 0 || s[2] < a->head_dim)
+// Rules every operand layout follows: non-negative strides, a row stride of at least
+// head_dim, strides in multiples of 8 elements (16-byte chunks stay aligned) and a 16-byte
+// aligned base.  Outputs also need positive batch and head strides where that dimension
+// has more than one entry, so that no two output rows share memory.
+int check_layout_rules(const char* name, const void* ptr, const elsa_layout& l, int B, int H, int N, int D,
+                       bool output, int64_t s[3]) {
+  resolve_layout(l, H, N, D, s);
+  if (s[0] < 0 || s[1] < 0 || s[2] < D)
     return fail(ELSA_ERR_INVALID, "%s layout (%lld, %lld, %lld) needs non-negative strides and a row stride >= "
                 "head_dim", name, (long long)s[0], (long long)s[1], (long long)s[2]);
+  if (output && ((B > 1 && s[0] == 0) || (H > 1 && s[1] == 0)))
+    return fail(ELSA_ERR_INVALID, "%s is an output: its batch and head strides must be positive", name);
   if ((s[0] | s[1] | s[2]) % 8 != 0 || reinterpret_cast<uintptr_t>(ptr) % 16 != 0)
     return fail(ELSA_ERR_INVALID, "%s: strides must be multiples of 8 elements and the pointer 16-byte aligned",
                 name);
+  return ELSA_OK;
+}
+
+int check_layout(const char* name, const void* ptr, const elsa_layout& l, const elsa_fwd_args* a,
+                 int64_t part_len, bool output) {
+  int64_t s[3];
+  int rc = check_layout_rules(name, ptr, l, a->batch, a->heads, a->seq_len, a->head_dim, output, s);
+  if (rc) return rc;
   if (part_len * s[2] * (int64_t)dtype_size(a->dtype) >= (int64_t(1) << 31))
     return fail(ELSA_ERR_UNSUPPORTED, "%s: a K partition spans >= 2 GiB (partition_len %lld x row stride %lld)",
                 name, (long long)part_len, (long long)s[2]);
@@ -234,10 +247,10 @@ int check_fwd_call(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
   if (!a->workspace || a->workspace_bytes < pl->workspace_bytes)
     return fail(ELSA_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", a->workspace_bytes,
                 pl->workspace_bytes);
-  if ((rc = check_layout("q", a->q, a->q_layout, a, pl->partition_len)) ||
-      (rc = check_layout("k", a->k, a->k_layout, a, pl->partition_len)) ||
-      (rc = check_layout("v", a->v, a->v_layout, a, pl->partition_len)) ||
-      (rc = check_layout("out", a->out, a->out_layout, a, pl->partition_len)))
+  if ((rc = check_layout("q", a->q, a->q_layout, a, pl->partition_len, false)) ||
+      (rc = check_layout("k", a->k, a->k_layout, a, pl->partition_len, false)) ||
+      (rc = check_layout("v", a->v, a->v_layout, a, pl->partition_len, false)) ||
+      (rc = check_layout("out", a->out, a->out_layout, a, pl->partition_len, true)))
     return rc;
   return ELSA_OK;
 }
@@ -249,16 +262,40 @@ int check_rows(const elsa_fwd_args* a, const elsa_fwd_plan& pl, int q_start, int
   return ELSA_OK;
 }
 
-int check_bwd(const elsa_bwd_args* a, bool need_grads) {
+// What a backward entry point reads and writes: q, k (row stats); + v, out, dout (dbias);
+// + dq, dk, dv (dq/dk/dv).
+enum BwdUse { kUseQK = 0, kUseDbias = 1, kUseGrads = 2 };
+
+int check_bwd_layout(const elsa_bwd_args* a, const char* name, const void* ptr, const elsa_layout& l, bool output) {
+  int64_t s[3];
+  return check_layout_rules(name, ptr, l, a->batch, a->heads, a->seq_len, a->head_dim, output, s);
+}
+
+int check_bwd(const elsa_bwd_args* a, BwdUse use) {
   if (!a) return fail(ELSA_ERR_INVALID, "null argument");
   int rc = check_common(a->batch, a->heads, a->seq_len, a->head_dim, a->dtype, a->q, a->k, a->v);
   if (rc) return rc;
   if ((rc = check_bias(a->bias))) return rc;
-  if (need_grads) {
+  if (use == kUseGrads) {
     if (!a->out || !a->dout || !a->dq || !a->dk || !a->dv)
       return fail(ELSA_ERR_INVALID, "out, dout, dq, dk and dv must be non-null device pointers");
     if (!a->row_m || !a->row_z) return fail(ELSA_ERR_INVALID, "row_m and row_z are required");
   }
+  if (use == kUseDbias && (!a->out || !a->dout || !a->row_m || !a->row_z))
+    return fail(ELSA_ERR_INVALID, "out, dout, row_m, row_z and dbias must be non-null");
+  if ((rc = check_bwd_layout(a, "q", a->q, a->q_layout, false)) ||
+      (rc = check_bwd_layout(a, "k", a->k, a->k_layout, false)))
+    return rc;
+  if (use == kUseQK) return ELSA_OK;
+  if ((rc = check_bwd_layout(a, "v", a->v, a->v_layout, false)) ||
+      (rc = check_bwd_layout(a, "out", a->out, a->out_layout, false)) ||
+      (rc = check_bwd_layout(a, "dout", a->dout, a->dout_layout, false)))
+    return rc;
+  if (use == kUseDbias) return ELSA_OK;
+  if ((rc = check_bwd_layout(a, "dq", a->dq, a->dq_layout, true)) ||
+      (rc = check_bwd_layout(a, "dk", a->dk, a->dk_layout, true)) ||
+      (rc = check_bwd_layout(a, "dv", a->dv, a->dv_layout, true)))
+    return rc;
   return ELSA_OK;
 }
 
@@ -286,6 +323,15 @@ elsa::BwdParams bwd_params(const elsa_bwd_args* a) {
   char* base = static_cast<char*>(a->workspace);
   p.d_row = reinterpret_cast<float*>(base);
   p.lse_row = reinterpret_cast<float*>(base + align256(rows * 4));
+  const int H = a->heads, N = a->seq_len, D = a->head_dim;
+  resolve_layout(a->q_layout, H, N, D, p.qs);
+  resolve_layout(a->k_layout, H, N, D, p.ks);
+  resolve_layout(a->v_layout, H, N, D, p.vs);
+  resolve_layout(a->out_layout, H, N, D, p.os);
+  resolve_layout(a->dout_layout, H, N, D, p.gs);
+  resolve_layout(a->dq_layout, H, N, D, p.dqs);
+  resolve_layout(a->dk_layout, H, N, D, p.dks);
+  resolve_layout(a->dv_layout, H, N, D, p.dvs);
   return p;
 }
 
@@ -352,7 +398,7 @@ size_t elsa_bwd_workspace_bytes(const elsa_bwd_args* a) {
 int elsa_bwd(const elsa_bwd_args* a, void* stream) { return elsa_bwd_stage(a, -1, stream); }
 
 int elsa_bwd_stage(const elsa_bwd_args* a, int32_t stage, void* stream) {
-  int rc = check_bwd(a, true);
+  int rc = check_bwd(a, kUseGrads);
   if (rc) return rc;
   if (stage < -1 || stage > 2) return fail(ELSA_ERR_INVALID, "stage must be -1, 0, 1 or 2 (got %d)", stage);
   const size_t need = elsa_bwd_workspace_bytes(a);
@@ -365,7 +411,7 @@ int elsa_bwd_stage(const elsa_bwd_args* a, int32_t stage, void* stream) {
 }
 
 int elsa_row_stats(const elsa_bwd_args* a, float* row_m, float* row_z, void* stream) {
-  int rc = check_bwd(a, false);
+  int rc = check_bwd(a, kUseQK);
   if (rc) return rc;
   if (!row_m || !row_z) return fail(ELSA_ERR_INVALID, "row_m and row_z must be non-null");
   hipError_t e = elsa::launch_row_stats(bwd_params(a), row_m, row_z, a->dtype, static_cast<hipStream_t>(stream));
@@ -385,10 +431,9 @@ size_t elsa_dbias_workspace_bytes(const elsa_bwd_args* a, int32_t bias_batch, in
 }
 
 int elsa_dbias(const elsa_bwd_args* a, float* dbias, int32_t bias_batch, int32_t bias_heads, void* stream) {
-  int rc = check_bwd(a, false);
+  int rc = check_bwd(a, kUseDbias);
   if (rc) return rc;
-  if (!a->out || !a->dout || !a->row_m || !a->row_z || !dbias)
-    return fail(ELSA_ERR_INVALID, "out, dout, row_m, row_z and dbias must be non-null");
+  if (!dbias) return fail(ELSA_ERR_INVALID, "out, dout, row_m, row_z and dbias must be non-null");
   if (!(bias_batch == 1 || bias_batch == a->batch) || !(bias_heads == 1 || bias_heads == a->heads))
     return fail(ELSA_ERR_INVALID, "dbias shape [%d,%d] does not broadcast against [%d,%d]", bias_batch, bias_heads,
                 a->batch, a->heads);

@@ -42,10 +42,12 @@ __device__ inline float load_bias_b(const BiasView& b, int bi, int hi, int row, 
   return static_cast<float>(static_cast<const bf16*>(b.ptr)[off]);
 }
 
-// Copy rows [row0, row0+TT) x [0, DP) of a [N, D] matrix into LDS, row-major
-// (stride RS) and/or transposed (stride TS); rows >= row_end and d >= D are zero.
+// Copy rows [row0, row0+TT) x [0, DP) of an [N, D] matrix with row stride rs (elements)
+// into LDS, row-major (stride RS) and/or transposed (stride TS); rows >= row_end and
+// d >= D are zero.
 template <typename T, int DP, int NT, bool RM, bool TR>
-__device__ inline void stage_tile(const T* __restrict__ src, int row0, int row_end, int D, T* rm, T* tr, int tid) {
+__device__ inline void stage_tile(const T* __restrict__ src, int64_t rs, int row0, int row_end, int D, T* rm, T* tr,
+                                  int tid) {
   using C = BwdCfg<T, DP>;
   constexpr int CPR = DP / C::CE;
   constexpr int TOTAL = C::TT * CPR;
@@ -54,7 +56,7 @@ __device__ inline void stage_tile(const T* __restrict__ src, int row0, int row_e
     const int r = ci / CPR, d0 = (ci % CPR) * C::CE;
     const int ra = row0 + r;
     Chunk16 v{};
-    if (ra < row_end && d0 < D) v = *reinterpret_cast<const Chunk16*>(src + (int64_t)ra * D + d0);
+    if (ra < row_end && d0 < D) v = *reinterpret_cast<const Chunk16*>(src + (int64_t)ra * rs + d0);
     const T* e = reinterpret_cast<const T*>(&v);
     if constexpr (RM) {
       if constexpr (C::HALF) {
@@ -88,8 +90,9 @@ template <typename T>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdParams p) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)p.BH * p.N) return;
-  const T* o = static_cast<const T*>(p.out) + i * p.D;
-  const T* g = static_cast<const T*>(p.dout) + i * p.D;
+  const int bh = (int)(i / p.N), row = (int)(i - (int64_t)bh * p.N), bi = bh / p.H, hi = bh - bi * p.H;
+  const T* o = static_cast<const T*>(p.out) + bi * p.os[0] + hi * p.os[1] + (int64_t)row * p.os[2];
+  const T* g = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1] + (int64_t)row * p.gs[2];
   float acc = 0.f;
   for (int d = 0; d < p.D; d += 16 / (int)sizeof(T)) {
     const Chunk16 a = *reinterpret_cast<const Chunk16*>(o + d);
@@ -126,20 +129,19 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
   const int wg_last = min(p.N, wg_row0 + BM) - 1;
   const int my_row = wg_row0 + wave * 32 + c;
   const bool row_ok = my_row < p.N;
-  const int64_t hoff = (int64_t)bh * p.N * p.D;
-  const T* Q = static_cast<const T*>(p.q) + hoff;
-  const T* K = static_cast<const T*>(p.k) + hoff;
-  const T* V = static_cast<const T*>(p.v) + hoff;
-  const T* dO = static_cast<const T*>(p.dout) + hoff;
   const int bi = bh / p.H, hi = bh % p.H;
+  const T* Q = static_cast<const T*>(p.q) + bi * p.qs[0] + hi * p.qs[1];
+  const T* K = static_cast<const T*>(p.k) + bi * p.ks[0] + hi * p.ks[1];
+  const T* V = static_cast<const T*>(p.v) + bi * p.vs[0] + hi * p.vs[1];
+  const T* dO = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1];
 
   F qf[C::NKK], gf[C::NKK];
   const int rsafe = row_ok ? my_row : 0;
 #pragma unroll
   for (int kk = 0; kk < C::NKK; ++kk) {
     const int d0 = kk * C::KSTEP + g * C::KP;
-    qf[kk] = load_frag<T>(Q + (int64_t)rsafe * p.D + d0, row_ok && d0 < p.D);
-    gf[kk] = load_frag<T>(dO + (int64_t)rsafe * p.D + d0, row_ok && d0 < p.D);
+    qf[kk] = load_frag<T>(Q + (int64_t)rsafe * p.qs[2] + d0, row_ok && d0 < p.D);
+    gf[kk] = load_frag<T>(dO + (int64_t)rsafe * p.gs[2] + d0, row_ok && d0 < p.D);
   }
   const float lse = row_ok ? p.lse_row[(int64_t)bh * p.N + my_row] : 0.f;
   const float dd = row_ok ? p.d_row[(int64_t)bh * p.N + my_row] : 0.f;
@@ -152,8 +154,8 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
 
   for (int t0 = 0; t0 < k_end; t0 += C::TT) {
     __syncthreads();
-    stage_tile<T, DP, NT, C::HALF, true>(K, t0, k_end, p.D, Ks, Kt, tid);
-    stage_tile<T, DP, NT, C::HALF, !C::HALF>(V, t0, k_end, p.D, Vs, Vt, tid);
+    stage_tile<T, DP, NT, C::HALF, true>(K, p.ks[2], t0, k_end, p.D, Ks, Kt, tid);
+    stage_tile<T, DP, NT, C::HALF, !C::HALF>(V, p.vs[2], t0, k_end, p.D, Vs, Vt, tid);
     __syncthreads();
     f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
     }
   }
   if (!row_ok) return;
-  T* out = static_cast<T*>(p.dq) + hoff + (int64_t)my_row * p.D;
+  T* out = static_cast<T*>(p.dq) + bi * p.dqs[0] + hi * p.dqs[1] + (int64_t)my_row * p.dqs[2];
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
@@ -218,20 +220,19 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dkdv_kernel(const BwdParams p)
   const int key0 = wg_key0 + wave * 32;
   const int my_key = key0 + c;
   const bool key_ok = my_key < p.N;
-  const int64_t hoff = (int64_t)bh * p.N * p.D;
-  const T* Q = static_cast<const T*>(p.q) + hoff;
-  const T* K = static_cast<const T*>(p.k) + hoff;
-  const T* V = static_cast<const T*>(p.v) + hoff;
-  const T* dO = static_cast<const T*>(p.dout) + hoff;
   const int bi = bh / p.H, hi = bh % p.H;
+  const T* Q = static_cast<const T*>(p.q) + bi * p.qs[0] + hi * p.qs[1];
+  const T* K = static_cast<const T*>(p.k) + bi * p.ks[0] + hi * p.ks[1];
+  const T* V = static_cast<const T*>(p.v) + bi * p.vs[0] + hi * p.vs[1];
+  const T* dO = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1];
 
   F kf[C::NKK], vf[C::NKK];
   const int ksafe = key_ok ? my_key : 0;
 #pragma unroll
   for (int kk = 0; kk < C::NKK; ++kk) {
     const int d0 = kk * C::KSTEP + g * C::KP;
-    kf[kk] = load_frag<T>(K + (int64_t)ksafe * p.D + d0, key_ok && d0 < p.D);
-    vf[kk] = load_frag<T>(V + (int64_t)ksafe * p.D + d0, key_ok && d0 < p.D);
+    kf[kk] = load_frag<T>(K + (int64_t)ksafe * p.ks[2] + d0, key_ok && d0 < p.D);
+    vf[kk] = load_frag<T>(V + (int64_t)ksafe * p.vs[2] + d0, key_ok && d0 < p.D);
   }
   f32x16 dk[C::NDT], dv[C::NDT];
 #pragma unroll
@@ -243,8 +244,8 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dkdv_kernel(const BwdParams p)
 
   for (int t0 = r_begin; t0 < p.N; t0 += C::TT) {
     __syncthreads();
-    stage_tile<T, DP, NT, C::HALF, true>(Q, t0, p.N, p.D, Qs, Qt, tid);
-    stage_tile<T, DP, NT, C::HALF, true>(dO, t0, p.N, p.D, Gs, Gt, tid);
+    stage_tile<T, DP, NT, C::HALF, true>(Q, p.qs[2], t0, p.N, p.D, Qs, Qt, tid);
+    stage_tile<T, DP, NT, C::HALF, true>(dO, p.gs[2], t0, p.N, p.D, Gs, Gt, tid);
     if (tid < C::TT) {
       const int ra = t0 + tid;
       lse_s[tid] = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : kNegInf;
@@ -293,8 +294,8 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dkdv_kernel(const BwdParams p)
     }
   }
   if (!key_ok) return;
-  T* okp = static_cast<T*>(p.dk) + hoff + (int64_t)my_key * p.D;
-  T* ovp = static_cast<T*>(p.dv) + hoff + (int64_t)my_key * p.D;
+  T* okp = static_cast<T*>(p.dk) + bi * p.dks[0] + hi * p.dks[1] + (int64_t)my_key * p.dks[2];
+  T* ovp = static_cast<T*>(p.dv) + bi * p.dvs[0] + hi * p.dvs[1] + (int64_t)my_key * p.dvs[2];
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
@@ -349,12 +350,11 @@ void bwd_dq_half_kernel(const BwdParams p) {
   const int wg_row0 = wg.x * BM;
   const int wg_last = min(p.N, wg_row0 + BM) - 1;
   const int row0 = wg_row0 + wave * ROWS_W;
-  const int64_t hoff = (int64_t)bh * p.N * p.D;
-  const T* Q = static_cast<const T*>(p.q) + hoff;
-  const T* K = static_cast<const T*>(p.k) + hoff;
-  const T* V = static_cast<const T*>(p.v) + hoff;
-  const T* dO = static_cast<const T*>(p.dout) + hoff;
   const int bi = bh / p.H, hi = bh % p.H;
+  const T* Q = static_cast<const T*>(p.q) + bi * p.qs[0] + hi * p.qs[1];
+  const T* K = static_cast<const T*>(p.k) + bi * p.ks[0] + hi * p.ks[1];
+  const T* V = static_cast<const T*>(p.v) + bi * p.vs[0] + hi * p.vs[1];
+  const T* dO = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1];
   const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
@@ -369,8 +369,8 @@ void bwd_dq_half_kernel(const BwdParams p) {
 #pragma unroll
     for (int kk = 0; kk < NKK; ++kk) {
       const int d0 = kk * 16 + g * 8;
-      qf[rt][kk] = load_frag<T>(Q + (int64_t)rs * p.D + d0, ok && d0 < p.D);
-      gf[rt][kk] = load_frag<T>(dO + (int64_t)rs * p.D + d0, ok && d0 < p.D);
+      qf[rt][kk] = load_frag<T>(Q + (int64_t)rs * p.qs[2] + d0, ok && d0 < p.D);
+      gf[rt][kk] = load_frag<T>(dO + (int64_t)rs * p.gs[2] + d0, ok && d0 < p.D);
     }
     lse[rt] = ok ? p.lse_row[(int64_t)bh * p.N + row] : __builtin_huge_valf();
     dd[rt] = ok ? p.d_row[(int64_t)bh * p.N + row] : 0.f;
@@ -385,9 +385,8 @@ static_for<0, NCH>([&](auto I) {
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
       if (t0 + r < k_end && d0 < p.D) {
-        const int64_t off = (int64_t)(t0 + r) * p.D + d0;
-        kreg[i] = *reinterpret_cast<const Chunk16*>(K + off);
-        vreg[i] = *reinterpret_cast<const Chunk16*>(V + off);
+        kreg[i] = *reinterpret_cast<const Chunk16*>(K + (int64_t)(t0 + r) * p.ks[2] + d0);
+        vreg[i] = *reinterpret_cast<const Chunk16*>(V + (int64_t)(t0 + r) * p.vs[2] + d0);
       } else {
         kreg[i] = Chunk16{};
         vreg[i] = Chunk16{};
@@ -491,7 +490,7 @@ static_for<0, NCH>([&](auto I) {
   for (int rt = 0; rt < RT; ++rt) {
     const int my_row = row0 + rt * 32 + c;
     if (my_row >= p.N) continue;
-    T* out = static_cast<T*>(p.dq) + hoff + (int64_t)my_row * p.D;
+    T* out = static_cast<T*>(p.dq) + bi * p.dqs[0] + hi * p.dqs[1] + (int64_t)my_row * p.dqs[2];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -531,12 +530,11 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
   const int bh = wg.y;
   const int wg_key0 = wg.x * BN;
   const int key0 = wg_key0 + wave * KEYS_W;
-  const int64_t hoff = (int64_t)bh * p.N * p.D;
-  const T* Q = static_cast<const T*>(p.q) + hoff;
-  const T* K = static_cast<const T*>(p.k) + hoff;
-  const T* V = static_cast<const T*>(p.v) + hoff;
-  const T* dO = static_cast<const T*>(p.dout) + hoff;
   const int bi = bh / p.H, hi = bh % p.H;
+  const T* Q = static_cast<const T*>(p.q) + bi * p.qs[0] + hi * p.qs[1];
+  const T* K = static_cast<const T*>(p.k) + bi * p.ks[0] + hi * p.ks[1];
+  const T* V = static_cast<const T*>(p.v) + bi * p.vs[0] + hi * p.vs[1];
+  const T* dO = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1];
   const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
@@ -550,8 +548,8 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
 #pragma unroll
     for (int kk = 0; kk < NKK; ++kk) {
       const int d0 = kk * 16 + g * 8;
-      kf[kt][kk] = load_frag<T>(K + (int64_t)ksafe * p.D + d0, key_ok[kt] && d0 < p.D);
-      vf[kt][kk] = load_frag<T>(V + (int64_t)ksafe * p.D + d0, key_ok[kt] && d0 < p.D);
+      kf[kt][kk] = load_frag<T>(K + (int64_t)ksafe * p.ks[2] + d0, key_ok[kt] && d0 < p.D);
+      vf[kt][kk] = load_frag<T>(V + (int64_t)ksafe * p.vs[2] + d0, key_ok[kt] && d0 < p.D);
     }
   }
   f32x16 dk[KRT][NDT], dv[KRT][NDT];
@@ -571,9 +569,8 @@ static_for<0, NCH>([&](auto I) {
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
       if (t0 + r < p.N && d0 < p.D) {
-        const int64_t off = (int64_t)(t0 + r) * p.D + d0;
-        qreg[i] = *reinterpret_cast<const Chunk16*>(Q + off);
-        greg[i] = *reinterpret_cast<const Chunk16*>(dO + off);
+        qreg[i] = *reinterpret_cast<const Chunk16*>(Q + (int64_t)(t0 + r) * p.qs[2] + d0);
+        greg[i] = *reinterpret_cast<const Chunk16*>(dO + (int64_t)(t0 + r) * p.gs[2] + d0);
       } else {
         qreg[i] = Chunk16{};
         greg[i] = Chunk16{};
@@ -692,8 +689,8 @@ static_for<0, NCH>([&](auto I) {
   for (int kt = 0; kt < KRT; ++kt) {
     const int my_key = key0 + kt * 32 + c;
     if (my_key >= p.N) continue;
-    T* okp = static_cast<T*>(p.dk) + hoff + (int64_t)my_key * p.D;
-    T* ovp = static_cast<T*>(p.dv) + hoff + (int64_t)my_key * p.D;
+    T* okp = static_cast<T*>(p.dk) + bi * p.dks[0] + hi * p.dks[1] + (int64_t)my_key * p.dks[2];
+    T* ovp = static_cast<T*>(p.dv) + bi * p.dvs[0] + hi * p.dvs[1] + (int64_t)my_key * p.dvs[2];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -729,21 +726,20 @@ __global__ __launch_bounds__(64 * WAVES) void row_stats_kernel(const BwdParams p
   const int wg_last = min(p.N, wg_row0 + BM) - 1;
   const int my_row = wg_row0 + wave * 32 + c;
   const bool row_ok = my_row < p.N;
-  const int64_t hoff = (int64_t)bh * p.N * p.D;
-  const T* Q = static_cast<const T*>(p.q) + hoff;
-  const T* K = static_cast<const T*>(p.k) + hoff;
   const int bi = bh / p.H, hi = bh % p.H;
+  const T* Q = static_cast<const T*>(p.q) + bi * p.qs[0] + hi * p.qs[1];
+  const T* K = static_cast<const T*>(p.k) + bi * p.ks[0] + hi * p.ks[1];
   F qf[C::NKK];
 #pragma unroll
   for (int kk = 0; kk < C::NKK; ++kk) {
     const int d0 = kk * C::KSTEP + g * C::KP;
-    qf[kk] = load_frag<T>(Q + (int64_t)(row_ok ? my_row : 0) * p.D + d0, row_ok && d0 < p.D);
+    qf[kk] = load_frag<T>(Q + (int64_t)(row_ok ? my_row : 0) * p.qs[2] + d0, row_ok && d0 < p.D);
   }
   float m_run = kNegInf, z_lane = 0.f;
   const int k_end = p.causal ? wg_last + 1 : p.N;
   for (int t0 = 0; t0 < k_end; t0 += C::TT) {
     __syncthreads();
-    stage_tile<T, DP, NT, C::HALF, !C::HALF>(K, t0, k_end, p.D, Ks, Kt, tid);
+    stage_tile<T, DP, NT, C::HALF, !C::HALF>(K, p.ks[2], t0, k_end, p.D, Ks, Kt, tid);
     __syncthreads();
     f32x16 s = f32x16{};
 #pragma unroll
@@ -801,20 +797,19 @@ __global__ __launch_bounds__(64) void dbias_kernel(const BwdParams p, float* dbi
     {
       const int b = b_lo + (int)(pair / nh), h = h_lo + (int)(pair % nh);
       const int bh = b * p.H + h;
-      const int64_t hoff = (int64_t)bh * p.N * p.D;
-      const T* Q = static_cast<const T*>(p.q) + hoff;
-      const T* K = static_cast<const T*>(p.k) + hoff;
-      const T* V = static_cast<const T*>(p.v) + hoff;
-      const T* dO = static_cast<const T*>(p.dout) + hoff;
+      const T* Q = static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1];
+      const T* K = static_cast<const T*>(p.k) + b * p.ks[0] + h * p.ks[1];
+      const T* V = static_cast<const T*>(p.v) + b * p.vs[0] + h * p.vs[1];
+      const T* dO = static_cast<const T*>(p.dout) + b * p.gs[0] + h * p.gs[1];
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int kk = 0; kk < C::NKK; ++kk) {
         const int d0 = kk * C::KSTEP + g * C::KP;
         const bool dok = d0 < p.D;
-        const auto qb = load_frag<T>(Q + (int64_t)(row_ok ? my_row : 0) * p.D + d0, row_ok && dok);
-        const auto gb = load_frag<T>(dO + (int64_t)(row_ok ? my_row : 0) * p.D + d0, row_ok && dok);
-        const auto ka = load_frag<T>(K + (int64_t)(krow_ok ? krow : 0) * p.D + d0, krow_ok && dok);
-        const auto va = load_frag<T>(V + (int64_t)(krow_ok ? krow : 0) * p.D + d0, krow_ok && dok);
+        const auto qb = load_frag<T>(Q + (int64_t)(row_ok ? my_row : 0) * p.qs[2] + d0, row_ok && dok);
+        const auto gb = load_frag<T>(dO + (int64_t)(row_ok ? my_row : 0) * p.gs[2] + d0, row_ok && dok);
+        const auto ka = load_frag<T>(K + (int64_t)(krow_ok ? krow : 0) * p.ks[2] + d0, krow_ok && dok);
+        const auto va = load_frag<T>(V + (int64_t)(krow_ok ? krow : 0) * p.vs[2] + d0, krow_ok && dok);
         s = M::mma(ka, qb, s);
         dp = M::mma(va, gb, dp);
       }

@@ -88,6 +88,8 @@ struct BwdParams {
   int causal;
   float scale;       // 1/sqrt(D_model)
   float scale_log2;  // scale * log2(e)
+  // element strides (batch, head, row) of q, k, v, out, dout and of dq, dk, dv
+  int64_t qs[3], ks[3], vs[3], os[3], gs[3], dqs[3], dks[3], dvs[3];
 };
 
 // stage < 0: preprocess, dq and dk/dv; 0: preprocess only; 1: dq only; 2: dk/dv only.

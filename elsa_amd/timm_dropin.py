@@ -124,20 +124,32 @@ class _SwinWindowCommon(nn.Module):
                                  relative_position_index(win_h, win_w, device=self.relative_position_bias_table.device),
                                  persistent=False)
 
-    def _qkv_and_bias(self, x: torch.Tensor, mask: Optional[torch.Tensor]):
-        batch_windows, seq_len, _ = x.shape
-        qkv = self.qkv(x).reshape(batch_windows, seq_len, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4)
-        q, k, v = qkv.unbind(0)
+    def _q_factor(self) -> float:
+        """Factor on q that turns the kernels' 1/sqrt(head_dim) into the module's own scale."""
         canonical_scale = self.head_dim ** -0.5
-        if abs(self.scale - canonical_scale) > 1e-12:
-            q = q * (self.scale / canonical_scale)
+        return 1.0 if abs(self.scale - canonical_scale) <= 1e-12 else self.scale / canonical_scale
+
+    def _qkv5(self, x: torch.Tensor) -> torch.Tensor:
+        """The fused projection as [B_win, N, 3, H, D]."""
+        batch_windows, seq_len, _ = x.shape
+        return self.qkv(x).reshape(batch_windows, seq_len, 3, self.num_heads, self.head_dim)
+
+    def _bias(self, mask: Optional[torch.Tensor], batch_windows: int, seq_len: int) -> torch.Tensor:
         bias = self._get_rel_pos_bias()
         if mask is not None:
             num_win = int(mask.shape[0])
             mask_bias = mask.view(1, num_win, 1, seq_len, seq_len).expand(
                 batch_windows // num_win, -1, self.num_heads, -1, -1)
             bias = bias + mask_bias.reshape(-1, self.num_heads, seq_len, seq_len)
-        return q, k, v, bias
+        return bias
+
+    def _qkv_and_bias(self, x: torch.Tensor, mask: Optional[torch.Tensor]):
+        batch_windows, seq_len, _ = x.shape
+        q, k, v = self._qkv5(x).permute(2, 0, 3, 1, 4).unbind(0)
+        factor = self._q_factor()
+        if factor != 1.0:
+            q = q * factor
+        return q, k, v, self._bias(mask, batch_windows, seq_len)
 
     def _out(self, y: torch.Tensor, batch_windows: int, seq_len: int) -> torch.Tensor:
         y = y.transpose(1, 2).reshape(batch_windows, seq_len, self.attn_dim)

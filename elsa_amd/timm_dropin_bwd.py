@@ -15,7 +15,7 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from .attention_bwd import twopass_attention_train
+from .attention_bwd import _train_bnhd, qkv_attention_train
 from .timm_dropin import _SwinWindowCommon, _patch, _swin_state, _vit_out, _vit_qkv, _vit_state
 
 
@@ -49,9 +49,15 @@ class ElsaTrainTimmVitAttention(nn.Module):
             raise ValueError("ELSA ViT bwd drop-in currently supports unmasked attention only")
         if self.training and getattr(self.attn_drop, "p", 0.0):
             raise ValueError("ELSA ViT bwd drop-in does not implement attention dropout")
-        q, k, v = _vit_qkv(self, x)
-        y = twopass_attention_train(q, k, v, **self._elsa_kwargs_for_seq(x.shape[1], q.dtype))
-        return _vit_out(self, y, x.shape[0], x.shape[1])
+        batch, seq_len, _ = x.shape
+        if isinstance(self.q_norm, nn.Identity) and isinstance(self.k_norm, nn.Identity):
+            # q, k, v straight from the fused projection; its gradient comes back in place
+            qkv = self.qkv(x).reshape(batch, seq_len, 3, self.num_heads, self.head_dim)
+            y = qkv_attention_train(qkv, **self._elsa_kwargs_for_seq(seq_len, qkv.dtype))
+        else:
+            q, k, v = _vit_qkv(self, x)
+            y = _train_bnhd(q, k, v, **self._elsa_kwargs_for_seq(seq_len, q.dtype))
+        return _vit_out(self, y, batch, seq_len)
 
 
 class ElsaTrainTimmSwinWindowAttention(_SwinWindowCommon):
@@ -70,9 +76,17 @@ class ElsaTrainTimmSwinWindowAttention(_SwinWindowCommon):
     def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         if self.training and self.attn_drop.p:
             raise ValueError("ELSA Swin bwd drop-in does not implement attention dropout")
-        q, k, v, bias = self._qkv_and_bias(x, mask)
-        y = twopass_attention_train(q, k, v, bias=bias, **self._elsa_kwargs_for_window(x.shape[1]))
-        return self._out(y, x.shape[0], x.shape[1])
+        batch_windows, seq_len, _ = x.shape
+        bias = self._bias(mask, batch_windows, seq_len)
+        kwargs = self._elsa_kwargs_for_window(seq_len)
+        qkv = self._qkv5(x)
+        factor = self._q_factor()
+        if factor == 1.0:
+            y = qkv_attention_train(qkv, bias=bias, **kwargs)
+        else:
+            q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+            y = _train_bnhd(q * factor, k, v, bias=bias, **kwargs)
+        return self._out(y, batch_windows, seq_len)
 
 
 def patch_timm_attention_train(model: nn.Module, *, elsa_kwargs: Optional[dict] = None) -> TrainPatchReport:

@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define ELSA_ABI_VERSION 2
+#define ELSA_ABI_VERSION 3
 
 typedef enum elsa_dtype { ELSA_F16 = 0, ELSA_BF16 = 1, ELSA_F32 = 2 } elsa_dtype;
 
@@ -72,8 +72,10 @@ typedef struct elsa_bias_desc {
 /* Element strides of a [B, H, N, D] operand whose last dimension is contiguous.
  * All zero means the dense layout (H*N*D, N*D, D).  Non-dense layouts let callers hand
  * over views without a copy, e.g. q/k/v sliced out of a fused [B, N, 3, H, D] projection
- * or an output written straight into [B, N, H, D].  Row strides must be multiples of 8
- * elements and base pointers 16-byte aligned. */
+ * or an output written straight into [B, N, H, D].  Strides must be multiples of 8
+ * elements, the row stride at least head_dim, and base pointers 16-byte aligned.
+ * Outputs (out; dq, dk, dv) must not alias themselves or each other: their strides are
+ * positive. */
 typedef struct elsa_layout {
   int64_t batch, head, row;
 } elsa_layout;
@@ -127,6 +129,10 @@ typedef struct elsa_bwd_args {
   int32_t _pad;
   void* workspace;       /* 2*B*H*N floats (D and LSE2 rows)                   */
   size_t workspace_bytes;
+  /* zero = dense [B,H,N,D].  The reference backward reads contiguous copies
+   * (attention_bwd.py:722-726); strided views avoid them. */
+  elsa_layout q_layout, k_layout, v_layout, out_layout, dout_layout;
+  elsa_layout dq_layout, dk_layout, dv_layout;
 } elsa_bwd_args;
 
 int elsa_abi_version(void);

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_struct_sizes():
     lib = _lib.load()
-    assert lib.elsa_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.elsa_abi_version() == _lib.ABI_VERSION == 3
     for which, st in _lib._STRUCTS.items():
         assert lib.elsa_struct_size(which) == ctypes.sizeof(st)
 
@@ -117,15 +117,43 @@ def test_bwd_and_dbias_reject_bad_args_without_launching():
     lib = _lib.load()
     b = _lib.BwdArgs()
     b.batch, b.heads, b.seq_len, b.head_dim, b.dtype = 1, 1, 64, 64, _lib.ELSA_F16
-    b.q = b.k = b.v = 1
+    b.q = b.k = b.v = 256
     assert lib.elsa_bwd(ctypes.byref(b), None) == _lib.ELSA_ERR_INVALID  # no out/dout/grads
-    b.out = b.dout = b.dq = b.dk = b.dv = b.row_m = b.row_z = 1
+    b.out = b.dout = b.dq = b.dk = b.dv = b.row_m = b.row_z = 256
     assert lib.elsa_bwd(ctypes.byref(b), None) == _lib.ELSA_ERR_WORKSPACE
     assert lib.elsa_bwd_workspace_bytes(ctypes.byref(b)) >= 2 * 64 * 4
     assert lib.elsa_dbias_workspace_bytes(ctypes.byref(b), 1, 1) >= lib.elsa_bwd_workspace_bytes(ctypes.byref(b))
     assert lib.elsa_dbias_workspace_bytes(ctypes.byref(b), 0, 1) == 0
     assert lib.elsa_dbias(ctypes.byref(b), 1, 2, 1, None) == _lib.ELSA_ERR_INVALID  # bias_batch 2 vs B=1
     assert lib.elsa_debug_mfma(5, 1, 1, 1, None) == _lib.ELSA_ERR_INVALID
+
+
+def test_bwd_layout_rules_without_launching():
+    lib = _lib.load()
+    b = _lib.BwdArgs()
+    b.batch, b.heads, b.seq_len, b.head_dim, b.dtype = 2, 3, 64, 64, _lib.ELSA_F16
+    b.q = b.k = b.v = b.out = b.dout = b.dq = b.dk = b.dv = b.row_m = b.row_z = 256
+    b.workspace, b.workspace_bytes = 256, 1 << 20  # never dereferenced: no kernel is launched
+    # a [B,N,3,H,D] view (row stride 3*H*D, head stride D) is a valid input and output layout
+    b.q_layout = _lib.Layout(64 * 3 * 3 * 64, 64, 3 * 3 * 64)
+    b.dq_layout = _lib.Layout(64 * 3 * 3 * 64, 64, 3 * 3 * 64)
+    assert lib.elsa_bwd_stage(ctypes.byref(b), 7, None) == _lib.ELSA_ERR_INVALID  # past the layout checks
+    assert "stage" in lib.elsa_last_error().decode()
+    b.k = 258  # misaligned base
+    assert lib.elsa_bwd(ctypes.byref(b), None) == _lib.ELSA_ERR_INVALID
+    assert "16-byte" in lib.elsa_last_error().decode()
+    b.k = 256
+    b.v_layout = _lib.Layout(3 * 64 * 64, 64 * 64, 60)  # row stride < head_dim
+    assert lib.elsa_bwd(ctypes.byref(b), None) == _lib.ELSA_ERR_INVALID
+    assert "row stride" in lib.elsa_last_error().decode()
+    b.v_layout = _lib.Layout(0, 0, 0)
+    b.dk_layout = _lib.Layout(3 * 64 * 64, 0, 64)  # heads of an output would share rows
+    assert lib.elsa_bwd(ctypes.byref(b), None) == _lib.ELSA_ERR_INVALID
+    assert "output" in lib.elsa_last_error().decode()
+    b.dk_layout = _lib.Layout(0, 0, 0)
+    b.k_layout = _lib.Layout(3 * 64 * 64, 0, 64)  # an input may broadcast over heads
+    assert lib.elsa_bwd_stage(ctypes.byref(b), 7, None) == _lib.ELSA_ERR_INVALID
+    assert "stage" in lib.elsa_last_error().decode()
 
 
 def test_python_api_validation_on_cpu_tensors():

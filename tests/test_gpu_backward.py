@@ -11,7 +11,7 @@ import torch
 import elsa_amd
 from elsa_amd.attention_bwd import _dense_bias_backward
 from oracle import elsa_oracle as O
-from tests.gpu_util import GRAD_TOL, assert_parity, describe, dev, host, max_abs, ulp
+from tests.gpu_util import GRAD_TOL, TORCH_DT, assert_parity, describe, dev, host, max_abs, ulp
 
 pytestmark = pytest.mark.gpu
 
@@ -173,3 +173,90 @@ def test_dbias_split_reduction_matches_unsplit_and_closed_form(bias_shape):
                "elsa_dbias")
     torch.cuda.synchronize()
     np.testing.assert_allclose(host(split).reshape(-1), host(unsplit).reshape(-1), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("dt,n,causal,d", [("fp16", 197, False, 64), ("bf16", 1025, True, 64), ("fp32", 300, False, 64),
+                                           ("fp16", 4097, True, 64), ("fp16", 49, False, 32), ("fp16", 300, False, 128)])
+def test_strided_backward_is_bitwise_the_dense_one(dt, n, causal, d):
+    """q, k, v as views of a fused [B,N,3,H,D] projection, out and dO as [B,N,H,D] memory,
+    and dq, dk, dv written into one fused [B,N,3,H,D] gradient: the same bits as the
+    backward on dense copies.  The kernels read and write through the layouts, no copy."""
+    from elsa_amd.attention import _BiasMeta
+    from elsa_amd.attention_bwd import _backward, _with_state
+
+    b, h = 2, 3
+    describe(f"strided backward {dt} n={n} causal={causal} d={d}")
+    g = torch.Generator().manual_seed(4242 + n)
+    qkv = (torch.randn((b, n, 3, h, d), generator=g) * 0.5).to(TORCH_DT[dt]).cuda()
+    do_bnhd = torch.randn((b, n, h, d), generator=g).to(qkv.dtype).cuda()
+    q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+    do = do_bnhd.permute(0, 2, 1, 3)
+    out, rm, rz = _with_state(q, k, v, is_causal=causal, out_bnhd=True)
+    assert out.stride()[1] == d and not out.is_contiguous()
+    meta = _BiasMeta(None, 0, 0, 0, 0, False)
+    dense = _backward(*(t.contiguous() for t in (q, k, v, out, do)), meta, is_causal=causal, row_m=rm, row_z=rz)
+    dqkv = torch.full_like(qkv, float("nan"))
+    grads = dqkv.permute(2, 0, 3, 1, 4).unbind(0)
+    ret = _backward(q, k, v, out, do, meta, is_causal=causal, row_m=rm, row_z=rz, grads=grads)
+    torch.cuda.synchronize()
+    assert all(r.data_ptr() == gr.data_ptr() for r, gr in zip(ret, grads))
+    for name, a, ref in zip("qkv", grads, dense):
+        assert torch.equal(a, ref), f"d{name} differs from the dense backward"
+    # the public entry point on the same views (dense outputs)
+    pub = elsa_amd.twopass_attention_backward(q, k, v, out, do, is_causal=causal, row_m=rm, row_z=rz)
+    for a, ref in zip(pub, dense):
+        assert torch.equal(a, ref)
+
+
+def test_strided_backward_with_head_broadcast_inputs():
+    """k and v broadcast over heads (zero head stride) are read in place; the gradients
+    per head match those of the materialised copies."""
+    from elsa_amd.attention import _BiasMeta
+    from elsa_amd.attention_bwd import _backward, _with_state
+
+    describe("strided backward, head-broadcast k/v")
+    g = torch.Generator().manual_seed(77)
+    b, h, n, d = 1, 4, 333, 64
+    q = torch.randn((b, h, n, d), generator=g).half().cuda()
+    k1 = torch.randn((b, 1, n, d), generator=g).half().cuda()
+    v1 = torch.randn((b, 1, n, d), generator=g).half().cuda()
+    do = torch.randn((b, h, n, d), generator=g).half().cuda()
+    k, v = k1.expand(b, h, n, d), v1.expand(b, h, n, d)
+    out, rm, rz = _with_state(q, k, v)
+    meta = _BiasMeta(None, 0, 0, 0, 0, False)
+    strided = _backward(q, k, v, out, do, meta, is_causal=False, row_m=rm, row_z=rz)
+    dense = _backward(q, k.contiguous(), v.contiguous(), out, do, meta, is_causal=False, row_m=rm, row_z=rz)
+    torch.cuda.synchronize()
+    for a, ref in zip(strided, dense):
+        assert torch.equal(a, ref)
+
+
+@pytest.mark.parametrize("dt,n,bias", [("fp16", 197, False), ("bf16", 49, True), ("fp32", 130, True)])
+def test_qkv_attention_train_matches_twopass_attention_train(dt, n, bias):
+    """The fused-qkv autograd path (the drop-ins' training path) gives the same output and
+    the same q/k/v (and bias) gradients, bit for bit, as twopass_attention_train on the
+    unbound views."""
+    from elsa_amd.attention_bwd import qkv_attention_train
+
+    b, h, d = 2, 3, 32 if n == 49 else 64
+    describe(f"qkv_attention_train {dt} n={n} bias={bias}")
+    g = torch.Generator().manual_seed(900 + n)
+    tdt = TORCH_DT[dt]
+    base = torch.randn((b, n, 3, h, d), generator=g).to(tdt).cuda()
+    do = torch.randn((b, h, n, d), generator=g).to(tdt).cuda()
+    bias_t = (torch.randn((1, h, n, n), generator=g) * 0.3).to(tdt).cuda() if bias else None
+
+    qkv1 = base.clone().requires_grad_(True)
+    bias1 = bias_t.clone().requires_grad_(True) if bias else None
+    out1 = qkv_attention_train(qkv1, bias=bias1)
+    out1.backward(do)
+    qkv2 = base.clone().requires_grad_(True)
+    bias2 = bias_t.clone().requires_grad_(True) if bias else None
+    q, k, v = qkv2.permute(2, 0, 3, 1, 4).unbind(0)
+    out2 = elsa_amd.twopass_attention_train(q, k, v, bias=bias2)
+    out2.backward(do)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+    assert qkv1.grad.is_contiguous() and torch.equal(qkv1.grad, qkv2.grad)
+    if bias:
+        assert torch.equal(bias1.grad, bias2.grad)
