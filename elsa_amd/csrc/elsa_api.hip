@@ -212,8 +212,9 @@ int run_phase(const elsa_fwd_args* a, const elsa_fwd_plan& pl, int q_start, int 
 }
 
 // Rules every operand layout follows: non-negative strides, a row stride of at least
-// head_dim, strides in multiples of 8 elements (16-byte chunks stay aligned) and a 16-byte
-// aligned base.  Outputs also need positive batch and head strides where that dimension
+// head_dim and below 2^25 elements (the kernels keep a 64-row stage's offsets in 32 bits),
+// strides in multiples of 8 elements (16-byte chunks stay aligned) and a 16-byte aligned
+// base.  Outputs also need positive batch and head strides where that dimension
 // has more than one entry, so that no two output rows share memory.
 int check_layout_rules(const char* name, const void* ptr, const elsa_layout& l, int B, int H, int N, int D,
                        bool output, int64_t s[3]) {
@@ -226,6 +227,8 @@ int check_layout_rules(const char* name, const void* ptr, const elsa_layout& l, 
   if ((s[0] | s[1] | s[2]) % 8 != 0 || reinterpret_cast<uintptr_t>(ptr) % 16 != 0)
     return fail(ELSA_ERR_INVALID, "%s: strides must be multiples of 8 elements and the pointer 16-byte aligned",
                 name);
+  if (s[2] >= (int64_t(1) << 25))
+    return fail(ELSA_ERR_UNSUPPORTED, "%s: row stride %lld is not below 2^25 elements", name, (long long)s[2]);
   return ELSA_OK;
 }
 

@@ -88,9 +88,11 @@ __device__ inline typename Mfma<T>::frag a_frag(const T* rm, const T* tr, int c,
 // ------------------------------------------------------------------ preprocess
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdParams p) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)p.BH * p.N) return;
-  const int bh = (int)(i / p.N), row = (int)(i - (int64_t)bh * p.N), bi = bh / p.H, hi = bh - bi * p.H;
+  // grid: x = 256-row block, y = batch * head
+  const int row = blockIdx.x * 256 + threadIdx.x, bh = blockIdx.y;
+  if (row >= p.N) return;
+  const int64_t i = (int64_t)bh * p.N + row;
+  const int bi = bh / p.H, hi = bh - bi * p.H;
   const T* o = static_cast<const T*>(p.out) + bi * p.os[0] + hi * p.os[1] + (int64_t)row * p.os[2];
   const T* g = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1] + (int64_t)row * p.gs[2];
   float acc = 0.f;
@@ -378,15 +380,27 @@ void bwd_dq_half_kernel(const BwdParams p) {
   }
   const int k_end = p.causal ? wg_last + 1 : p.N;
 
+  // element offsets of this thread's staging chunks inside a stage (row strides are
+  // below 2^25 elements, checked by the API, so 64 rows fit in 32 bits)
+  int32_t koff[NCH], voff[NCH];
+  static_for<0, NCH>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    const int ci = tid + i * NT;
+    const int r = ci / CPR, d0 = (ci % CPR) * 8;
+    koff[i] = r * (int32_t)p.ks[2] + d0;
+    voff[i] = r * (int32_t)p.vs[2] + d0;
+  });
   Chunk16 kreg[NCH], vreg[NCH];
   auto gload = [&](int t0) {
+    const T* kt = K + (int64_t)t0 * p.ks[2];
+    const T* vt = V + (int64_t)t0 * p.vs[2];
 static_for<0, NCH>([&](auto I) {
       constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
       if (t0 + r < k_end && d0 < p.D) {
-        kreg[i] = *reinterpret_cast<const Chunk16*>(K + (int64_t)(t0 + r) * p.ks[2] + d0);
-        vreg[i] = *reinterpret_cast<const Chunk16*>(V + (int64_t)(t0 + r) * p.vs[2] + d0);
+        kreg[i] = *reinterpret_cast<const Chunk16*>(kt + koff[i]);
+        vreg[i] = *reinterpret_cast<const Chunk16*>(vt + voff[i]);
       } else {
         kreg[i] = Chunk16{};
         vreg[i] = Chunk16{};
@@ -561,16 +575,28 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
       dv[kt][dt] = f32x16{};
     }
 
+  // element offsets of this thread's staging chunks inside a stage (row strides are
+  // below 2^25 elements, checked by the API, so 64 rows fit in 32 bits)
+  int32_t qoff[NCH], goff[NCH];
+  static_for<0, NCH>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    const int ci = tid + i * NT;
+    const int r = ci / CPR, d0 = (ci % CPR) * 8;
+    qoff[i] = r * (int32_t)p.qs[2] + d0;
+    goff[i] = r * (int32_t)p.gs[2] + d0;
+  });
   Chunk16 qreg[NCH], greg[NCH];
   float lreg = 0.f, dreg = 0.f;
   auto gload = [&](int t0) {
+    const T* qt = Q + (int64_t)t0 * p.qs[2];
+    const T* gt = dO + (int64_t)t0 * p.gs[2];
 static_for<0, NCH>([&](auto I) {
       constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
       if (t0 + r < p.N && d0 < p.D) {
-        qreg[i] = *reinterpret_cast<const Chunk16*>(Q + (int64_t)(t0 + r) * p.qs[2] + d0);
-        greg[i] = *reinterpret_cast<const Chunk16*>(dO + (int64_t)(t0 + r) * p.gs[2] + d0);
+        qreg[i] = *reinterpret_cast<const Chunk16*>(qt + qoff[i]);
+        greg[i] = *reinterpret_cast<const Chunk16*>(gt + goff[i]);
       } else {
         qreg[i] = Chunk16{};
         greg[i] = Chunk16{};
@@ -847,8 +873,7 @@ __global__ __launch_bounds__(256) void dbias_reduce_kernel(const float* part, fl
 // ------------------------------------------------------------------ launchers
 template <typename T>
 static hipError_t pre_launch(const BwdParams& p, hipStream_t st) {
-  const int64_t rows = (int64_t)p.BH * p.N;
-  hipLaunchKernelGGL(bwd_pre_kernel<T>, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(bwd_pre_kernel<T>, dim3((unsigned)((p.N + 255) / 256), (unsigned)p.BH), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 

@@ -73,7 +73,8 @@ typedef struct elsa_bias_desc {
  * All zero means the dense layout (H*N*D, N*D, D).  Non-dense layouts let callers hand
  * over views without a copy, e.g. q/k/v sliced out of a fused [B, N, 3, H, D] projection
  * or an output written straight into [B, N, H, D].  Strides must be multiples of 8
- * elements, the row stride at least head_dim, and base pointers 16-byte aligned.
+ * elements, the row stride at least head_dim and below 2^25, and base pointers 16-byte
+ * aligned.
  * Outputs (out; dq, dk, dv) must not alias themselves or each other: their strides are
  * positive. */
 typedef struct elsa_layout {
