@@ -88,22 +88,31 @@ __device__ inline typename Mfma<T>::frag a_frag(const T* rm, const T* tr, int c,
 // ------------------------------------------------------------------ preprocess
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdParams p) {
-  // grid: x = 256-row block, y = batch * head
-  const int row = blockIdx.x * 256 + threadIdx.x, bh = blockIdx.y;
-  if (row >= p.N) return;
-  const int64_t i = (int64_t)bh * p.N + row;
+  // grid: x = block of 32 rows, y = batch * head.  The 8 lanes of a row read its 16-byte
+  // chunks side by side (lane j takes chunks j, j + 8, ...), so every load instruction
+  // covers whole 128-byte row segments, and add their partial sums with three xor shuffles.
+  constexpr int CE = 16 / (int)sizeof(T);
+  const int sub = threadIdx.x & 7, row = blockIdx.x * 32 + (threadIdx.x >> 3), bh = blockIdx.y;
+  const bool ok = row < p.N;  // uniform over the 8 lanes of a row: no lane leaves before the shuffles
   const int bi = bh / p.H, hi = bh - bi * p.H;
-  const T* o = static_cast<const T*>(p.out) + bi * p.os[0] + hi * p.os[1] + (int64_t)row * p.os[2];
-  const T* g = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1] + (int64_t)row * p.gs[2];
   float acc = 0.f;
-  for (int d = 0; d < p.D; d += 16 / (int)sizeof(T)) {
-    const Chunk16 a = *reinterpret_cast<const Chunk16*>(o + d);
-    const Chunk16 b = *reinterpret_cast<const Chunk16*>(g + d);
-    const T* ea = reinterpret_cast<const T*>(&a);
-    const T* eb = reinterpret_cast<const T*>(&b);
+  if (ok) {
+    const T* o = static_cast<const T*>(p.out) + bi * p.os[0] + hi * p.os[1] + (int64_t)row * p.os[2];
+    const T* g = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1] + (int64_t)row * p.gs[2];
+    for (int d = sub * CE; d < p.D; d += 8 * CE) {
+      const Chunk16 a = *reinterpret_cast<const Chunk16*>(o + d);
+      const Chunk16 b = *reinterpret_cast<const Chunk16*>(g + d);
+      const T* ea = reinterpret_cast<const T*>(&a);
+      const T* eb = reinterpret_cast<const T*>(&b);
 #pragma unroll
-    for (int t = 0; t < 16 / (int)sizeof(T); ++t) acc = fmaf(static_cast<float>(ea[t]), static_cast<float>(eb[t]), acc);
+      for (int t = 0; t < CE; ++t) acc = fmaf(static_cast<float>(ea[t]), static_cast<float>(eb[t]), acc);
+    }
   }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  acc += __shfl_xor(acc, 4);
+  if (!ok || sub != 0) return;
+  const int64_t i = (int64_t)bh * p.N + row;
   p.d_row[i] = acc;
   // LSE2 = m + log2(max(z, 1e-30)) (attention_bwd.py:224); a row with no valid key
   // (z == 0) stores +inf instead of -inf so that p = exp2(s - LSE2) is 0 without a test.
@@ -873,7 +882,7 @@ __global__ __launch_bounds__(256) void dbias_reduce_kernel(const float* part, fl
 // ------------------------------------------------------------------ launchers
 template <typename T>
 static hipError_t pre_launch(const BwdParams& p, hipStream_t st) {
-  hipLaunchKernelGGL(bwd_pre_kernel<T>, dim3((unsigned)((p.N + 255) / 256), (unsigned)p.BH), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(bwd_pre_kernel<T>, dim3((unsigned)((p.N + 31) / 32), (unsigned)p.BH), dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
