@@ -15,6 +15,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libelsa_hip.so"
+TORCH_MODULE_PATH = Path(__file__).resolve().parent / "_elsa_torch.so"
 
 ELSA_F16, ELSA_BF16, ELSA_F32 = 0, 1, 2
 ELSA_OK, ELSA_ERR_INVALID, ELSA_ERR_WORKSPACE, ELSA_ERR_LAUNCH, ELSA_ERR_UNSUPPORTED = 0, -1, -2, -3, -4
@@ -181,6 +182,30 @@ def load() -> ctypes.CDLL:
                                f"({lib.elsa_struct_size(which)} != {ctypes.sizeof(st)})")
     _lib = lib
     return lib
+
+
+_torch_module = None
+
+
+def torch_module():
+    """The C++ autograd module (_elsa_torch.so, built by elsa_amd.build next to libelsa_hip.so).
+
+    Loads libelsa_hip.so first, so both share that one copy of the library (its SONAME)."""
+    global _torch_module
+    if _torch_module is None:
+        import importlib.util
+
+        load()
+        if not TORCH_MODULE_PATH.exists():
+            raise RuntimeError(f"{TORCH_MODULE_PATH} is missing: run `python -m elsa_amd.build` (or "
+                               "__graft_entry__.build()) to compile it")
+        spec = importlib.util.spec_from_file_location("elsa_amd._elsa_torch", TORCH_MODULE_PATH)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        if mod.abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{TORCH_MODULE_PATH}: ABI version {mod.abi_version()} != {ABI_VERSION}")
+        _torch_module = mod
+    return _torch_module
 
 
 def check(status: int, what: str) -> None:

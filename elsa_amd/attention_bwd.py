@@ -63,21 +63,18 @@ def _with_state(q, k, v, *, bias=None, is_causal=False, block_m=None, block_n=No
     """twopass_attention_with_state; ``out_bnhd`` returns out as a [B,H,N,D] view of [B,N,H,D] memory."""
     _check_qkv(q, k, v, "twopass_attention_with_state")
     batch, heads, seq_len, head_dim = map(int, q.shape)
-    if seq_len <= 0:
+    if seq_len > 0:
+        part, qc, sdt = _state_options(q, block_m=block_m, block_n=block_n, q_chunk_size=q_chunk_size,
+                                       summary_dtype=summary_dtype, phase1_warps=phase1_warps,
+                                       phase2_warps=phase2_warps, phase1_stages=phase1_stages,
+                                       phase2_stages=phase2_stages, input_precision=input_precision,
+                                       algorithm=algorithm)
+    else:
         empty_state = torch.empty((batch * heads, 0), device=q.device, dtype=torch.float32)
         out_empty = torch.empty_like(q)
         if return_contiguous_inputs:
             return out_empty, empty_state, empty_state, q.contiguous(), k.contiguous(), v.contiguous()
         return out_empty, empty_state, empty_state
-    if head_dim > 128:
-        raise ValueError("head_dim > 128 is not supported by the current Triton kernels")
-    if algorithm not in ("auto", "paper_scan"):
-        raise ValueError("only algorithm='paper_scan' is available in this strict release")
-    part, qc, sdt = _resolve_forward_options(
-        q, block_m=block_m, block_n=block_n, q_chunk_size=q_chunk_size, summary_dtype=summary_dtype,
-        phase1_warps=phase1_warps, phase2_warps=phase2_warps, phase1_stages=phase1_stages,
-        phase2_stages=phase2_stages, input_precision=input_precision,
-    )
     out, row_m, row_z, q_c, k_c, v_c = _elsa_forward(
         q, k, v, bias=bias, is_causal=is_causal, summary_dtype=sdt, partition_len=part, q_chunk=qc, want_state=True,
         out_bnhd=out_bnhd,
@@ -85,6 +82,21 @@ def _with_state(q, k, v, *, bias=None, is_causal=False, block_m=None, block_n=No
     if return_contiguous_inputs:
         return out, row_m, row_z, q_c.contiguous(), k_c.contiguous(), v_c.contiguous()
     return out, row_m, row_z
+
+
+def _state_options(q, *, block_m, block_n, q_chunk_size, summary_dtype, phase1_warps, phase2_warps, phase1_stages,
+                   phase2_stages, input_precision, algorithm):
+    """Validation and routing of twopass_attention_with_state (attention_bwd.py:77-185): returns
+    (partition_len, q_chunk, summary_dtype)."""
+    if int(q.shape[-1]) > 128:
+        raise ValueError("head_dim > 128 is not supported by the current Triton kernels")
+    if algorithm not in ("auto", "paper_scan"):
+        raise ValueError("only algorithm='paper_scan' is available in this strict release")
+    return _resolve_forward_options(
+        q, block_m=block_m, block_n=block_n, q_chunk_size=q_chunk_size, summary_dtype=summary_dtype,
+        phase1_warps=phase1_warps, phase2_warps=phase2_warps, phase1_stages=phase1_stages,
+        phase2_stages=phase2_stages, input_precision=input_precision,
+    )
 
 
 def _bwd_args(q_c, k_c, v_c, out_c, do_c, row_m, row_z, dq, dk, dv, bias_meta, *, is_causal, scale):
@@ -348,7 +360,23 @@ def qkv_attention_train(qkv: torch.Tensor, *, bias: Optional[torch.Tensor] = Non
         raise ValueError("qkv must have shape [B,N,3,H,D]")
     bwd_kwargs = _split_train_kwargs(bwd_block_m, bwd_block_n, bwd_num_warps, bwd_num_stages, bwd_input_precision,
                                      fwd_kwargs)
+    q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
+    _check_qkv(q, k, v, "qkv_attention_train")
     _check_bwd_kwargs(bwd_kwargs, qkv.dtype)
+    batch, heads, seq_len, head_dim = map(int, q.shape)
+    if seq_len > 0 and head_dim % 8 == 0 and qkv.is_contiguous() and qkv.data_ptr() % 16 == 0:
+        # the whole call in C++ (elsa_torch.cpp): no Python between the launches of either pass
+        opts = dict(block_m=None, block_n=None, q_chunk_size=None, summary_dtype=None, phase1_warps=None,
+                    phase2_warps=None, phase1_stages=None, phase2_stages=None, input_precision="auto",
+                    algorithm="auto")
+        unknown = set(fwd_kwargs) - set(opts)
+        if unknown:
+            raise TypeError(f"qkv_attention_train() got unexpected keyword arguments {sorted(unknown)}")
+        opts.update(fwd_kwargs)
+        part, qc, sdt = _state_options(q, **opts)
+        meta = _canonical_bias(bias, batch=batch, heads=heads, seq_len=seq_len, device=q.device)
+        return _lib.torch_module().qkv_attention_train(qkv, meta.tensor, bool(is_causal), _lib.dtype_code(sdt),
+                                                       int(part or 0), int(qc or 0))
     return _TwopassQkvAutograd.apply(qkv, bias, is_causal, dict(fwd_kwargs), bwd_kwargs)
 
 

@@ -1,0 +1,201 @@
+// PyTorch autograd function of the fused-qkv training path (host code only).
+//
+// The timm drop-ins train through q, k, v = qkv[:, :, 0..2] of a [B, N, 3, H, D]
+// projection.  This function keeps the whole host side of one training call in C++:
+//   forward   planner query, workspace, elsa_fwd with row state, out as [B, N, H, D]
+//   backward  elsa_bwd writing dq, dk, dv into one [B, N, 3, H, D] gradient, and
+//             elsa_dbias when the bias needs a gradient
+// so that no Python runs between the launches and the backward needs no interpreter lock
+// on autograd's device thread.  It mirrors _TwopassQkvAutograd in attention_bwd.py (the
+// Python twin, used where this module cannot take the call) and the reference's
+// _TwopassAttentionAutograd (attention_bwd.py:842-905).
+#include <ATen/hip/HIPContext.h>
+#include <torch/extension.h>
+
+#include <array>
+
+#include "elsa_hip.h"
+
+namespace {
+
+using torch::autograd::AutogradContext;
+using torch::autograd::tensor_list;
+
+int32_t code_of(at::ScalarType t) {
+  switch (t) {
+    case at::kHalf: return ELSA_F16;
+    case at::kBFloat16: return ELSA_BF16;
+    case at::kFloat: return ELSA_F32;
+    default: TORCH_CHECK(false, "supported dtypes are fp16, bf16, and fp32");
+  }
+  return -1;
+}
+
+void check(int rc, const char* what) {
+  TORCH_CHECK(rc == ELSA_OK, what, " failed (status ", rc, "): ", elsa_last_error());
+}
+
+void* current_stream() { return at::hip::getCurrentHIPStream().stream(); }
+
+elsa_layout layout_of(const at::Tensor& t) { return elsa_layout{t.stride(0), t.stride(1), t.stride(2)}; }
+
+// The layout rules of the C ABI (a dense last dimension, strides in multiples of 8
+// elements, a 16-byte aligned base); anything else is read from a dense copy.
+at::Tensor operand(const at::Tensor& t) {
+  const bool ok = t.stride(3) == 1 && t.stride(0) % 8 == 0 && t.stride(1) % 8 == 0 && t.stride(2) % 8 == 0 &&
+                  t.stride(0) >= 0 && t.stride(1) >= 0 && t.stride(2) >= t.size(3) && t.stride(2) < (1 << 25) &&
+                  reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 == 0;
+  return ok ? t : t.contiguous();
+}
+
+// bias: [1|B, 1|H, N, N], broadcast by zero strides
+elsa_bias_desc bias_desc(const at::Tensor& bias) {
+  elsa_bias_desc b{};
+  b.dtype = ELSA_F32;
+  if (!bias.defined()) return b;
+  b.ptr = bias.data_ptr();
+  b.dtype = code_of(bias.scalar_type());
+  b.stride_b = bias.size(0) == 1 ? 0 : bias.stride(0);
+  b.stride_h = bias.size(1) == 1 ? 0 : bias.stride(1);
+  b.stride_q = bias.stride(2);
+  b.stride_k = bias.stride(3);
+  return b;
+}
+
+// [B, H, N, D] views of the q, k, v slices of a [B, N, 3, H, D] tensor
+std::array<at::Tensor, 3> unbind_qkv(const at::Tensor& qkv) {
+  const at::Tensor t = qkv.permute({2, 0, 3, 1, 4});
+  return {t[0], t[1], t[2]};
+}
+
+at::Tensor bytes(const at::Tensor& like, size_t n) {
+  return at::empty({static_cast<int64_t>(n)}, like.options().dtype(at::kByte));
+}
+
+class QkvAttention : public torch::autograd::Function<QkvAttention> {
+ public:
+  // bias is optional: an absent bias must not reach apply() as an undefined tensor, which
+  // autograd would treat as an input variable
+  static at::Tensor forward(AutogradContext* ctx, const at::Tensor& qkv, const c10::optional<at::Tensor>& bias_opt,
+                            bool causal, int64_t summary_dtype, int64_t partition_len, int64_t q_chunk) {
+    const c10::DeviceGuard guard(qkv.device());
+    const at::Tensor bias = bias_opt.has_value() ? *bias_opt : at::Tensor();
+    const auto qkv_v = unbind_qkv(qkv);
+    const at::Tensor &q = qkv_v[0], &k = qkv_v[1], &v = qkv_v[2];
+    const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
+    at::Tensor out = at::empty({B, N, H, D}, qkv.options()).permute({0, 2, 1, 3});
+    const auto f32 = qkv.options().dtype(at::kFloat);
+    at::Tensor row_m = at::empty({B * H, N}, f32), row_z = at::empty({B * H, N}, f32);
+
+    elsa_fwd_args a{};
+    a.q = q.data_ptr();
+    a.k = k.data_ptr();
+    a.v = v.data_ptr();
+    a.out = out.data_ptr();
+    a.row_m = row_m.data_ptr<float>();
+    a.row_z = row_z.data_ptr<float>();
+    a.bias = bias_desc(bias);
+    a.batch = static_cast<int32_t>(B);
+    a.heads = static_cast<int32_t>(H);
+    a.seq_len = static_cast<int32_t>(N);
+    a.head_dim = static_cast<int32_t>(D);
+    a.dtype = code_of(qkv.scalar_type());
+    a.summary_dtype = static_cast<int32_t>(summary_dtype);
+    a.is_causal = causal ? 1 : 0;
+    a.partition_len = static_cast<int32_t>(partition_len);
+    a.q_chunk = static_cast<int32_t>(q_chunk);
+    a.scale = 0.f;  // 1 / sqrt(head_dim)
+    a.q_layout = layout_of(q);
+    a.k_layout = layout_of(k);
+    a.v_layout = layout_of(v);
+    a.out_layout = layout_of(out);
+    elsa_fwd_plan plan;
+    check(elsa_fwd_plan_get(&a, &plan), "elsa_fwd_plan_get");
+    const at::Tensor ws = bytes(qkv, plan.workspace_bytes);
+    a.workspace = ws.data_ptr();
+    a.workspace_bytes = plan.workspace_bytes;
+    check(elsa_fwd(&a, current_stream()), "elsa_fwd");
+
+    ctx->save_for_backward({qkv, out, row_m, row_z, bias});
+    ctx->saved_data["causal"] = causal;
+    return out;
+  }
+
+  static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
+    const auto saved = ctx->get_saved_variables();
+    const at::Tensor &qkv = saved[0], &out = saved[1], &row_m = saved[2], &row_z = saved[3], &bias = saved[4];
+    const bool causal = ctx->saved_data["causal"].toBool();
+    const c10::DeviceGuard guard(qkv.device());
+    const at::Tensor dout = operand(grads[0]);
+    const auto qkv_v = unbind_qkv(qkv);
+    const at::Tensor &q = qkv_v[0], &k = qkv_v[1], &v = qkv_v[2];
+    at::Tensor dqkv = at::empty(qkv.sizes(), qkv.options());
+    const auto d_v = unbind_qkv(dqkv);
+    const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
+
+    elsa_bwd_args b{};
+    b.q = q.data_ptr();
+    b.k = k.data_ptr();
+    b.v = v.data_ptr();
+    b.out = out.data_ptr();
+    b.dout = dout.data_ptr();
+    b.row_m = row_m.data_ptr<float>();
+    b.row_z = row_z.data_ptr<float>();
+    b.dq = d_v[0].data_ptr();
+    b.dk = d_v[1].data_ptr();
+    b.dv = d_v[2].data_ptr();
+    b.bias = bias_desc(bias);
+    b.batch = static_cast<int32_t>(B);
+    b.heads = static_cast<int32_t>(H);
+    b.seq_len = static_cast<int32_t>(N);
+    b.head_dim = static_cast<int32_t>(D);
+    b.dtype = code_of(qkv.scalar_type());
+    b.is_causal = causal ? 1 : 0;
+    b.scale = 0.f;
+    b.q_layout = layout_of(q);
+    b.k_layout = layout_of(k);
+    b.v_layout = layout_of(v);
+    b.out_layout = layout_of(out);
+    b.dout_layout = layout_of(dout);
+    b.dq_layout = layout_of(d_v[0]);
+    b.dk_layout = layout_of(d_v[1]);
+    b.dv_layout = layout_of(d_v[2]);
+    const size_t ws_bytes = elsa_bwd_workspace_bytes(&b);
+    const at::Tensor ws = bytes(qkv, ws_bytes);
+    b.workspace = ws.data_ptr();
+    b.workspace_bytes = ws_bytes;
+    check(elsa_bwd(&b, current_stream()), "elsa_bwd");
+
+    at::Tensor dbias;
+    if (bias.defined() && ctx->needs_input_grad(1)) {
+      const int32_t bb = static_cast<int32_t>(bias.size(0)), bhd = static_cast<int32_t>(bias.size(1));
+      at::Tensor d32 = at::empty({bb, bhd, N, N}, qkv.options().dtype(at::kFloat));
+      const size_t need = elsa_dbias_workspace_bytes(&b, bb, bhd);
+      const at::Tensor ws2 = bytes(qkv, need);
+      b.workspace = ws2.data_ptr();
+      b.workspace_bytes = need;
+      check(elsa_dbias(&b, d32.data_ptr<float>(), bb, bhd, current_stream()), "elsa_dbias");
+      dbias = d32.to(bias.scalar_type());
+    }
+    return {dqkv, dbias, at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor()};
+  }
+};
+
+at::Tensor qkv_attention_train(const at::Tensor& qkv, const c10::optional<at::Tensor>& bias, bool causal,
+                               int64_t summary_dtype, int64_t partition_len, int64_t q_chunk) {
+  TORCH_CHECK(qkv.dim() == 5 && qkv.size(2) == 3, "qkv must have shape [B,N,3,H,D]");
+  TORCH_CHECK(qkv.is_contiguous(), "qkv must be contiguous");
+  TORCH_CHECK(!bias.has_value() || bias->dim() == 4, "bias must be a canonical [1|B,1|H,N,N] view");
+  TORCH_CHECK(!bias.has_value() || bias->device() == qkv.device(), "bias must live on the same device as qkv");
+  return QkvAttention::apply(qkv, bias, causal, summary_dtype, partition_len, q_chunk);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "C++ autograd function of the fused-qkv ELSA training path";
+  m.def("qkv_attention_train", &qkv_attention_train, "fused-qkv two-pass attention with recompute backward");
+  m.def("current_stream", [] { return reinterpret_cast<int64_t>(current_stream()); },
+        "raw handle of the stream the launches go to");
+  m.def("abi_version", [] { return elsa_abi_version(); });
+}

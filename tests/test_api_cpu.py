@@ -31,6 +31,12 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
 
 
+def test_torch_module_loads_with_the_library_abi():
+    mod = _lib.torch_module()
+    assert mod.abi_version() == _lib.ABI_VERSION
+    assert callable(mod.qkv_attention_train) and callable(mod.current_stream)
+
+
 def test_abi_version_and_struct_sizes():
     lib = _lib.load()
     assert lib.elsa_abi_version() == _lib.ABI_VERSION == 3

@@ -260,3 +260,44 @@ def test_qkv_attention_train_matches_twopass_attention_train(dt, n, bias):
     assert qkv1.grad.is_contiguous() and torch.equal(qkv1.grad, qkv2.grad)
     if bias:
         assert torch.equal(bias1.grad, bias2.grad)
+
+
+def test_torch_module_launches_on_the_current_stream():
+    """The C++ autograd module enqueues on the stream torch considers current, also inside
+    a side-stream context."""
+    from elsa_amd import _lib
+
+    mod = _lib.torch_module()
+    assert mod.current_stream() == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert mod.current_stream() == side.cuda_stream
+
+
+@pytest.mark.parametrize("dt,bias", [("fp16", False), ("bf16", True)])
+def test_cpp_and_python_fused_qkv_paths_agree(dt, bias):
+    """qkv_attention_train's C++ autograd function and its Python twin give the same bits."""
+    from elsa_amd.attention_bwd import _TwopassQkvAutograd, qkv_attention_train
+
+    describe(f"C++ vs Python fused-qkv autograd {dt} bias={bias}")
+    g = torch.Generator().manual_seed(31)
+    b, n, h, d = 2, 197, 3, 64
+    base = torch.randn((b, n, 3, h, d), generator=g).to(TORCH_DT[dt]).cuda()
+    do = torch.randn((b, h, n, d), generator=g).to(TORCH_DT[dt]).cuda()
+    bias_t = (torch.randn((1, h, n, n), generator=g) * 0.3).to(TORCH_DT[dt]).cuda() if bias else None
+    res = []
+    for use_cpp in (True, False):
+        qkv = base.clone().requires_grad_(True)
+        bt = bias_t.clone().requires_grad_(True) if bias else None
+        if use_cpp:
+            out = qkv_attention_train(qkv, bias=bt)
+        else:
+            out = _TwopassQkvAutograd.apply(qkv, bt, False, {}, {})
+        out.backward(do)
+        res.append((out.detach(), qkv.grad, bt.grad if bias else None))
+    torch.cuda.synchronize()
+    (o1, g1, b1), (o2, g2, b2) = res
+    assert o1.stride() == o2.stride() and torch.equal(o1, o2)
+    assert torch.equal(g1, g2)
+    if bias:
+        assert torch.equal(b1, b2)
