@@ -327,8 +327,11 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
 // The row sum accumulates the fp32 p values; the MFMA takes them rounded to T.
 constexpr float kLazyTau = 8.0f;
 
+// 2 waves per SIMD, except the 1- and 2-wave variants at D >= 64 (sequences of at most 64
+// keys): their register staging of a whole 64-key stage does not fit that budget.
 template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void phase1_half_kernel(const Phase1Params p) {
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu((WAVES <= 2 && DP >= 64) ? 1 : 2, 2)))
+void phase1_half_kernel(const Phase1Params p) {
   using M = Mfma<T>;
   typedef typename M::frag F;
   constexpr int KT = 64;          // keys per LDS stage
