@@ -220,6 +220,10 @@ def main() -> int:
     print("bench: kernels " + ", ".join(f"{k_}={v_:.3f}ms" for k_, v_ in kern_ms.items()), file=sys.stderr,
           flush=True)
 
+    # ---- latency ratio against PyTorch's SDPA on the same inputs, the reference's headline
+    # comparison (README.md:55-58: ELSA / FlashAttention on A100), for fp16 only
+    vs_sdpa = _vs_sdpa(args, q, k, v, do, causal) if args.dtype == "fp16" else None
+
     # ---- sampled parity check of this very run (closed form, fp64 on CPU)
     rows = np.random.default_rng(0).choice(N, 16, replace=False)
     qs = q[:, :, rows].float().cpu().double().numpy()
@@ -309,6 +313,8 @@ def main() -> int:
         "kernels": kernels,
         "roofline": roofline,
     }
+    if vs_sdpa is not None:
+        result["vs_sdpa"] = vs_sdpa
     if args.vit_img:
         from elsa_amd.vision_models import vit_tiny_patch16
 
@@ -334,6 +340,48 @@ def main() -> int:
         result["cpu_baseline"] = _cpu_baseline(args, B, H, N, D, causal)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def _vs_sdpa(args, q, k, v, do, causal):
+    """Mean latency of the public API calls against torch.nn.functional.scaled_dot_product_attention
+    (PyTorch picks its fused kernel on ROCm), forward and forward+backward, timed the same way;
+    backward = (forward+backward) - forward.  lat_ratio = ELSA / SDPA, as the reference reports."""
+    import torch
+    import torch.nn.functional as F
+
+    import elsa_amd
+
+    iters = max(5, min(args.steps, 20))
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters
+
+    qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+
+    def sdpa_fb():
+        F.scaled_dot_product_attention(qg, kg, vg, is_causal=causal).backward(do)
+
+    def elsa_fb():
+        elsa_amd.twopass_attention_train(qg, kg, vg, is_causal=causal).backward(do)
+
+    with torch.no_grad():
+        s_f = timed(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=causal))
+        e_f = timed(lambda: elsa_amd.twopass_attention(q, k, v, is_causal=causal))
+    s_fb, e_fb = timed(sdpa_fb), timed(elsa_fb)
+    out = {"sdpa_fwd_ms": round(s_f, 4), "sdpa_bwd_ms": round(s_fb - s_f, 4),
+           "elsa_fwd_ms": round(e_f, 4), "elsa_bwd_ms": round(e_fb - e_f, 4),
+           "fwd_lat_ratio": round(e_f / s_f, 3), "bwd_lat_ratio": round((e_fb - e_f) / (s_fb - s_f), 3)}
+    print(f"bench: vs SDPA {out}", file=sys.stderr, flush=True)
+    return out
 
 
 def _vision_bench(args, dt, builder, imgs, label, tokens):
