@@ -366,14 +366,7 @@ def qkv_attention_train(qkv: torch.Tensor, *, bias: Optional[torch.Tensor] = Non
     batch, heads, seq_len, head_dim = map(int, q.shape)
     if seq_len > 0 and head_dim % 8 == 0 and qkv.is_contiguous() and qkv.data_ptr() % 16 == 0:
         # the whole call in C++ (elsa_torch.cpp): no Python between the launches of either pass
-        opts = dict(block_m=None, block_n=None, q_chunk_size=None, summary_dtype=None, phase1_warps=None,
-                    phase2_warps=None, phase1_stages=None, phase2_stages=None, input_precision="auto",
-                    algorithm="auto")
-        unknown = set(fwd_kwargs) - set(opts)
-        if unknown:
-            raise TypeError(f"qkv_attention_train() got unexpected keyword arguments {sorted(unknown)}")
-        opts.update(fwd_kwargs)
-        part, qc, sdt = _state_options(q, **opts)
+        part, qc, sdt = _state_options(q, **_fwd_options(fwd_kwargs, "qkv_attention_train"))
         meta = _canonical_bias(bias, batch=batch, heads=heads, seq_len=seq_len, device=q.device)
         return _lib.torch_module().qkv_attention_train(qkv, meta.tensor, bool(is_causal), _lib.dtype_code(sdt),
                                                        int(part or 0), int(qc or 0))
@@ -397,7 +390,36 @@ def _train_bnhd(q, k, v, *, bias=None, is_causal=False, bwd_block_m=None, bwd_bl
     """twopass_attention_train with out returned as a [B,H,N,D] view of [B,N,H,D] memory."""
     bwd_kwargs = _split_train_kwargs(bwd_block_m, bwd_block_n, bwd_num_warps, bwd_num_stages, bwd_input_precision,
                                      fwd_kwargs)
-    return _TwopassAttentionAutograd.apply(q, k, v, bias, is_causal, dict(fwd_kwargs), bwd_kwargs, True)
+    return _train(q, k, v, bias, is_causal, dict(fwd_kwargs), bwd_kwargs, True)
+
+
+_FWD_OPTION_DEFAULTS = dict(block_m=None, block_n=None, q_chunk_size=None, summary_dtype=None, phase1_warps=None,
+                            phase2_warps=None, phase1_stages=None, phase2_stages=None, input_precision="auto",
+                            algorithm="auto")
+
+
+def _fwd_options(fwd_kwargs, who):
+    unknown = set(fwd_kwargs) - set(_FWD_OPTION_DEFAULTS)
+    if unknown:
+        raise TypeError(f"{who}() got unexpected keyword arguments {sorted(unknown)}")
+    opts = dict(_FWD_OPTION_DEFAULTS)
+    opts.update(fwd_kwargs)
+    return opts
+
+
+def _train(q, k, v, bias, is_causal, fwd_kwargs, bwd_kwargs, out_bnhd):
+    """Autograd forward + recompute backward.  Inputs the kernels read in place take the C++
+    autograd function (elsa_torch.cpp); the rest (head dims that need a padded copy, empty
+    sequences) the Python one."""
+    _check_qkv(q, k, v, "twopass_attention_with_state")
+    batch, heads, seq_len, _ = map(int, q.shape)
+    if seq_len > 0 and all(_operand(t) is t for t in (q, k, v)):
+        part, qc, sdt = _state_options(q, **_fwd_options(fwd_kwargs, "twopass_attention_train"))
+        _check_bwd_kwargs(bwd_kwargs, q.dtype)
+        meta = _canonical_bias(bias, batch=batch, heads=heads, seq_len=seq_len, device=q.device)
+        return _lib.torch_module().attention_train(q, k, v, meta.tensor, bool(is_causal), _lib.dtype_code(sdt),
+                                                   int(part or 0), int(qc or 0), bool(out_bnhd))
+    return _TwopassAttentionAutograd.apply(q, k, v, bias, is_causal, dict(fwd_kwargs), bwd_kwargs, out_bnhd)
 
 
 def twopass_attention_train(
@@ -417,4 +439,4 @@ def twopass_attention_train(
     """Autograd wrapper: two-pass forward with state plus recompute backward (attention_bwd.py:1003-1030)."""
     bwd_kwargs = _split_train_kwargs(bwd_block_m, bwd_block_n, bwd_num_warps, bwd_num_stages, bwd_input_precision,
                                      fwd_kwargs)
-    return _TwopassAttentionAutograd.apply(q, k, v, bias, is_causal, dict(fwd_kwargs), bwd_kwargs)
+    return _train(q, k, v, bias, is_causal, dict(fwd_kwargs), bwd_kwargs, False)

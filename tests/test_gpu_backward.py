@@ -301,3 +301,30 @@ def test_cpp_and_python_fused_qkv_paths_agree(dt, bias):
     assert torch.equal(g1, g2)
     if bias:
         assert torch.equal(b1, b2)
+
+
+@pytest.mark.parametrize("dt,causal,bias", [("fp16", True, False), ("bf16", False, True), ("fp32", False, False)])
+def test_cpp_and_python_training_paths_agree(dt, causal, bias):
+    """twopass_attention_train's C++ autograd function and its Python twin give the same bits."""
+    from elsa_amd.attention_bwd import _TwopassAttentionAutograd
+
+    describe(f"C++ vs Python training autograd {dt} causal={causal} bias={bias}")
+    g = torch.Generator().manual_seed(57)
+    b, h, n, d = 2, 3, 300, 64
+    base = [torch.randn((b, h, n, d), generator=g).to(TORCH_DT[dt]).cuda() for _ in range(3)]
+    do = torch.randn((b, h, n, d), generator=g).to(TORCH_DT[dt]).cuda()
+    bias_t = (torch.randn((h, n, n), generator=g) * 0.3).to(TORCH_DT[dt]).cuda() if bias else None
+    res = []
+    for use_cpp in (True, False):
+        q, k, v = (t.clone().requires_grad_(True) for t in base)
+        bt = bias_t.clone().requires_grad_(True) if bias else None
+        if use_cpp:
+            out = elsa_amd.twopass_attention_train(q, k, v, bias=bt, is_causal=causal)
+        else:
+            out = _TwopassAttentionAutograd.apply(q, k, v, bt, causal, {}, {})
+        out.backward(do)
+        res.append((out.detach(), q.grad, k.grad, v.grad, bt.grad if bias else None))
+    torch.cuda.synchronize()
+    for a, ref in zip(res[0], res[1]):
+        if ref is not None:
+            assert torch.equal(a, ref)
