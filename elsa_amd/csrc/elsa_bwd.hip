@@ -85,6 +85,49 @@ __device__ inline typename Mfma<T>::frag a_frag(const T* rm, const T* tr, int c,
   }
 }
 
+// fp32 stage staging, double-buffered: each thread first loads its 16-byte chunks of the
+// next TT rows into registers (f32_stage_load, issued before the current stage's MFMAs),
+// then writes them transposed ([DP][TS], TS = TT + 1) into the other LDS buffer
+// (f32_stage_store).  Rows >= row_end and d >= D read as zeros.
+template <int DP, int NT>
+struct F32Stage {
+  static constexpr int CPR = DP / 4;              // 16-byte chunks per row
+  static constexpr int TOTAL = BwdCfg<float, DP>::TT * CPR;
+  static constexpr int NCH = (TOTAL + NT - 1) / NT;  // chunks per thread
+};
+
+template <int DP, int NT, int NR>
+__device__ inline void f32_stage_load(Chunk16 (&reg)[NR], const float* __restrict__ src, int64_t rs, int row0,
+                                      int row_end, int D, int tid) {
+  using S = F32Stage<DP, NT>;
+  static_assert(NR == S::NCH, "one register chunk per staged chunk of this thread");
+  static_for<0, S::NCH>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    const int ci = tid + i * NT;
+    const int r = ci / S::CPR, d0 = (ci % S::CPR) * 4;
+    Chunk16 v{};
+    if (ci < S::TOTAL && row0 + r < row_end && d0 < D)
+      v = *reinterpret_cast<const Chunk16*>(src + (int64_t)(row0 + r) * rs + d0);
+    reg[i] = v;
+  });
+}
+
+template <int DP, int NT, int NR>
+__device__ inline void f32_stage_store(const Chunk16 (&reg)[NR], float* tr, int tid) {
+  using S = F32Stage<DP, NT>;
+  static_assert(NR == S::NCH, "one register chunk per staged chunk of this thread");
+  constexpr int TS = BwdCfg<float, DP>::TS;
+  static_for<0, S::NCH>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    const int ci = tid + i * NT;
+    if (S::TOTAL % NT == 0 || ci < S::TOTAL) {
+      const int r = ci / S::CPR, d0 = (ci % S::CPR) * 4;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) tr[(d0 + t) * TS + r] = __uint_as_float(reg[i][t]);
+    }
+  });
+}
+
 // ------------------------------------------------------------------ preprocess
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdParams p) {
@@ -211,17 +254,17 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
 }
 
 // ------------------------------------------------------------------ dk / dv
+// fp32 only (the fp16 / bf16 kernels follow below).
 template <typename T, int DP, int WAVES, bool HAS_BIAS>
 __global__ __launch_bounds__(64 * WAVES) void bwd_dkdv_kernel(const BwdParams p) {
+  static_assert(sizeof(T) == 4, "fp32 kernel");
   using C = BwdCfg<T, DP>;
   using M = Mfma<T>;
   typedef typename M::frag F;
   constexpr int NT = 64 * WAVES, BN = 32 * WAVES;
-  __shared__ __attribute__((aligned(16))) T Qs[C::HALF ? C::TT * C::RS : 1];
-  __shared__ __attribute__((aligned(16))) T Gs[C::HALF ? C::TT * C::RS : 1];
-  __shared__ __attribute__((aligned(16))) T Qt[DP * C::TS];
-  __shared__ __attribute__((aligned(16))) T Gt[DP * C::TS];
-  __shared__ float lse_s[C::TT], dd_s[C::TT];
+  __shared__ __attribute__((aligned(16))) T Qt[2][DP * C::TS];
+  __shared__ __attribute__((aligned(16))) T Gt[2][DP * C::TS];
+  __shared__ float lse_s[2][C::TT], dd_s[2][C::TT];
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
@@ -252,57 +295,70 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dkdv_kernel(const BwdParams p)
     dv[dt] = f32x16{};
   }
   const int r_begin = p.causal ? (wg_key0 / C::TT) * C::TT : 0;
-
-  for (int t0 = r_begin; t0 < p.N; t0 += C::TT) {
-    __syncthreads();
-    stage_tile<T, DP, NT, C::HALF, true>(Q, p.qs[2], t0, p.N, p.D, Qs, Qt, tid);
-    stage_tile<T, DP, NT, C::HALF, true>(dO, p.gs[2], t0, p.N, p.D, Gs, Gt, tid);
+  const int ntiles = (p.N - r_begin + C::TT - 1) / C::TT;
+  Chunk16 qreg[F32Stage<DP, NT>::NCH], greg[F32Stage<DP, NT>::NCH];
+  float lreg = 0.f, dreg = 0.f;
+  auto gload = [&](int t0) {
+    f32_stage_load<DP, NT>(qreg, Q, p.qs[2], t0, p.N, p.D, tid);
+    f32_stage_load<DP, NT>(greg, dO, p.gs[2], t0, p.N, p.D, tid);
     if (tid < C::TT) {
       const int ra = t0 + tid;
-      lse_s[tid] = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : kNegInf;
-      dd_s[tid] = ra < p.N ? p.d_row[(int64_t)bh * p.N + ra] : 0.f;
+      lreg = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : kNegInf;
+      dreg = ra < p.N ? p.d_row[(int64_t)bh * p.N + ra] : 0.f;
     }
-    __syncthreads();
+  };
+  auto sstore = [&](int buf) {
+    f32_stage_store<DP, NT>(qreg, Qt[buf], tid);
+    f32_stage_store<DP, NT>(greg, Gt[buf], tid);
+    if (tid < C::TT) {
+      lse_s[buf][tid] = lreg;
+      dd_s[buf][tid] = dreg;
+    }
+  };
+  if (ntiles > 0) {
+    gload(r_begin);
+    sstore(0);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int t0 = r_begin + it * C::TT, buf = it & 1;
+    const bool has_next = it + 1 < ntiles;
+    if (has_next) gload(t0 + C::TT);
+    const T* qt = Qt[buf];
+    const T* gt = Gt[buf];
     f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < C::NKK; ++kk) {
-      s = M::mma(a_frag<T, DP>(Qs, Qt, c, g, kk), kf[kk], s);
-      dp = M::mma(a_frag<T, DP>(Gs, Gt, c, g, kk), vf[kk], dp);
+      s = M::mma(a_frag<T, DP>(nullptr, qt, c, g, kk), kf[kk], s);
+      dp = M::mma(a_frag<T, DP>(nullptr, gt, c, g, kk), vf[kk], dp);
     }
     f32x16 pv;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int rl = key_of_reg(r, g);
       const int row = t0 + rl;
-      const float lse = lse_s[rl];
+      const float lse = lse_s[buf][rl];
       bool ok = key_ok && row < p.N && lse > kNegInf;
       if (p.causal) ok = ok && row >= my_key;
       float x = s[r] * p.scale_log2;
       if constexpr (HAS_BIAS) x = ok ? fmaf(load_bias_b(p.bias, bi, hi, row, my_key), kLog2e, x) : x;
       const float pr = ok ? fast_exp2(x - lse) : 0.f;
       pv[r] = pr;
-      s[r] = pr * (dp[r] - dd_s[rl]);
+      s[r] = pr * (dp[r] - dd_s[buf][rl]);
     }
 #pragma unroll
     for (int j = 0; j < C::NJ; ++j) {
-      F bp, bs;
-      if constexpr (C::KP == 1) {
-        bp = pv[j];
-        bs = s[j];
-      } else {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          bp[t] = static_cast<T>(pv[j * 8 + t]);
-          bs[t] = static_cast<T>(s[j * 8 + t]);
-        }
-      }
+      const F bp = pv[j], bs = s[j];
 #pragma unroll
       for (int dt = 0; dt < C::NDT; ++dt) {
         const int off = (dt * 32 + c) * C::TS + key_of_reg(j * C::KP, g);
-        dv[dt] = M::mma(load_frag<T>(Gt + off, true), bp, dv[dt]);
-        dk[dt] = M::mma(load_frag<T>(Qt + off, true), bs, dk[dt]);
+        dv[dt] = M::mma(load_frag<T>(gt + off, true), bp, dv[dt]);
+        dk[dt] = M::mma(load_frag<T>(qt + off, true), bs, dk[dt]);
       }
     }
+    if (has_next) sstore(buf ^ 1);
+    __syncthreads();
   }
   if (!key_ok) return;
   T* okp = static_cast<T*>(p.dk) + bi * p.dks[0] + hi * p.dks[1] + (int64_t)my_key * p.dks[2];

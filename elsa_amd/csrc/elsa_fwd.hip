@@ -622,15 +622,12 @@ __device__ inline void mono_merge(float ma, float za, const float (&sa)[8], floa
 }
 
 template <typename ST, typename TO>
+// Grid: x = block of 256 (row, 8-column chunk) pairs of one (batch, head), y = batch * head.
 __global__ __launch_bounds__(256) void phase2_kernel(const Phase2Params p) {
   const int cpr = p.D >> 3;
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t total = (int64_t)p.BH * p.q_len * cpr;
-  if (gid >= total) return;
-  const int ch = (int)(gid % cpr);
-  const int64_t rl = gid / cpr;
-  const int r = (int)(rl % p.q_len);
-  const int bh = (int)(rl / p.q_len);
+  const int lid = blockIdx.x * 256 + threadIdx.x, bh = blockIdx.y;
+  if (lid >= p.q_len * cpr) return;
+  const int r = lid / cpr, ch = lid - r * cpr;
   const int row = p.q_start + r;
   int kb_hi = p.P - 1;
   if (p.causal) kb_hi = min(kb_hi, row / p.part_len);
@@ -656,12 +653,33 @@ __global__ __launch_bounds__(256) void phase2_kernel(const Phase2Params p) {
         for (int t = 0; t < 8; ++t) s[i][t] = 0.f;
       }
     }
-    // up-sweep: level widths 4, 2, 1; out[i] = merge(in[2i], in[2i+1])
+    // up-sweep: level widths 4, 2, 1; out[i] = merge(in[2i], in[2i+1]).  Leaves past kb_hi
+    // are the identity (-inf, 0, 0), and merging with the identity returns the other operand
+    // bit for bit, so those merges are skipped (n = live entries of the current level).
+    int n = min(8, kb_hi - base + 1);
 #pragma unroll
-    for (int w = 4; w >= 1; w >>= 1)
+    for (int w = 4; w >= 1; w >>= 1) {
 #pragma unroll
-      for (int i = 0; i < w; ++i) mono_merge(m[2 * i], z[2 * i], s[2 * i], m[2 * i + 1], z[2 * i + 1], s[2 * i + 1], m[i], z[i], s[i]);
-    mono_merge(am, az, as, m[0], z[0], s[0], am, az, as);
+      for (int i = 0; i < w; ++i) {
+        if (2 * i + 1 < n) {
+          mono_merge(m[2 * i], z[2 * i], s[2 * i], m[2 * i + 1], z[2 * i + 1], s[2 * i + 1], m[i], z[i], s[i]);
+        } else if (2 * i < n) {
+          m[i] = m[2 * i];
+          z[i] = z[2 * i];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) s[i][t] = s[2 * i][t];
+        }
+      }
+      n = (n + 1) >> 1;
+    }
+    if (base == 0) {
+      am = m[0];
+      az = z[0];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) as[t] = s[0][t];
+    } else {
+      mono_merge(am, az, as, m[0], z[0], s[0], am, az, as);
+    }
   }
 
   const int bi = bh / p.H, hi = bh - bi * p.H;
@@ -737,8 +755,7 @@ hipError_t launch_phase1(const Phase1Params& p, int dtype, int waves, hipStream_
 
 template <typename ST, typename TO>
 static hipError_t launch2(const Phase2Params& p, hipStream_t st) {
-  const int64_t total = (int64_t)p.BH * p.q_len * (p.D >> 3);
-  const dim3 grid((unsigned)((total + 255) / 256));
+  const dim3 grid((unsigned)((p.q_len * (p.D >> 3) + 255) / 256), (unsigned)p.BH);
   hipLaunchKernelGGL((phase2_kernel<ST, TO>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
