@@ -1,0 +1,71 @@
+"""CPU tests of bench.py's host logic: the single-GPU contract and the HBM-traffic
+calibration that turns FETCH_SIZE / WRITE_SIZE counters into bytes per launch."""
+from __future__ import annotations
+
+import csv
+import json
+import math
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+
+import bench  # noqa: E402
+
+
+def test_more_than_one_gpu_is_refused_with_a_message():
+    proc = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                          timeout=300, cwd=ROOT)
+    assert proc.returncode == 2
+    assert "single GPU" in proc.stderr and proc.stdout == ""
+
+
+def _write_counters(path: Path, counter: str, rows):
+    with open(path, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for i, (name, value) in enumerate(rows):
+            w.writerow({"Dispatch_Id": i, "Kernel_Name": name, "Counter_Name": counter, "Counter_Value": value})
+
+
+def test_traffic_calibration_scales_each_counter_by_the_copy_kernel(tmp_path):
+    """A counter that sees half of the memory channels reads half of a 1 GiB copy; every kernel's
+    figure is scaled by the same factor, and kernels are averaged over their dispatches."""
+    copy = "void at::native::vectorized_elementwise_kernel<4, at::native::CUDAFunctor_add<float>>"
+    fetch_rows = [("_ZN4elsa18phase1_half_kernelIDF16_Li64ELi2ELi4ELb0EEEvNS_12Phase1ParamsE", 1000.0),
+                  ("_ZN4elsa18phase1_half_kernelIDF16_Li64ELi2ELi4ELb0EEEvNS_12Phase1ParamsE", 1200.0),
+                  ("_ZN4elsa13phase2_kernelIDF16_DF16_EEvNS_12Phase2ParamsE", 300.0),
+                  ("some_other_kernel", 5.0),
+                  (copy, 1024 * 1024 / 2)]            # sees half of the 1 GiB read
+    write_rows = [("_ZN4elsa18phase1_half_kernelIDF16_Li64ELi2ELi4ELb0EEEvNS_12Phase1ParamsE", 700.0),
+                  ("_ZN4elsa18phase1_half_kernelIDF16_Li64ELi2ELi4ELb0EEEvNS_12Phase1ParamsE", 700.0),
+                  ("_ZN4elsa13phase2_kernelIDF16_DF16_EEvNS_12Phase2ParamsE", 100.0),
+                  (copy, 1024 * 1024)]                # sees all of the 1 GiB write
+    _write_counters(tmp_path / "f.csv", "FETCH_SIZE", fetch_rows)
+    _write_counters(tmp_path / "w.csv", "WRITE_SIZE", write_rows)
+    out = bench.summarize_pmc(str(tmp_path / "f.csv"), str(tmp_path / "w.csv"), 1024, str(tmp_path / "t.json"))
+    assert out["fetch_size_factor"] == 2.0 and out["write_size_factor"] == 1.0
+    p1 = out["phase1_fold"]
+    assert p1["dispatches"] == 2
+    assert math.isclose(p1["fetch_size_bytes"], 1100.0 * 2 * 1024)
+    assert math.isclose(p1["write_size_bytes"], 700.0 * 1024)
+    assert p1["hbm_bytes_per_launch"] == round(1100.0 * 2 * 1024 + 700.0 * 1024)
+    assert math.isclose(out["phase2_merge"]["fetch_size_bytes"], 300.0 * 2 * 1024)
+    assert "some_other_kernel" not in json.dumps(out)
+    assert json.loads((tmp_path / "t.json").read_text()) == json.loads(json.dumps(out))
+
+
+def test_traffic_calibration_needs_the_copy_kernel(tmp_path):
+    _write_counters(tmp_path / "f.csv", "FETCH_SIZE", [("_ZN4elsa13phase2_kernelIDF16_DF16_EE", 1.0)])
+    _write_counters(tmp_path / "w.csv", "WRITE_SIZE", [("_ZN4elsa13phase2_kernelIDF16_DF16_EE", 1.0)])
+    with pytest.raises(SystemExit, match="calibration"):
+        bench.summarize_pmc(str(tmp_path / "f.csv"), str(tmp_path / "w.csv"), 1024, str(tmp_path / "t.json"))
+
+
+def test_algorithmic_flops():
+    assert bench._flops_fwd(1, 8, 16384, 64, False) == 4.0 * 8 * 16384 ** 2 * 64
+    assert bench._flops_fwd(1, 1, 4, 2, True) == 4.0 * 2 * (4 * 5 / 2)
