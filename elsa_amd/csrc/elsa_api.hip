@@ -73,9 +73,7 @@ int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
 
   const int64_t n = a->seq_len, bh = (int64_t)a->batch * a->heads, d = a->head_dim;
   const int dp = elsa::pad_head_dim(a->head_dim);
-  const int rows_w = elsa::phase1_rows_per_wave(a->dtype, dp);
-  const int waves = n <= 64 ? 64 / rows_w : 4;
-  const int bm = rows_w * waves;
+  const int bm = elsa::phase1_block_m(a->dtype, dp, n);
   const int kt = elsa::phase1_key_tile(a->dtype, dp);
   const size_t row_bytes = 8 + (size_t)d * dtype_size(a->summary_dtype);
 
@@ -182,7 +180,7 @@ int run_phase(const elsa_fwd_args* a, const elsa_fwd_plan& pl, int q_start, int 
     p.scale_log2 = (float)(1.4426950408889634 * softmax_scale(a->scale, a->head_dim));
     p.bias_log2 = 1.4426950408889634f;
     p.rows_pad = pl.q_chunk;
-    hipError_t e = elsa::launch_phase1(p, a->dtype, pl.block_m / elsa::phase1_rows_per_wave(a->dtype, elsa::pad_head_dim(a->head_dim)), st);
+    hipError_t e = elsa::launch_phase1(p, a->dtype, pl.block_m, st);
     if (e != hipSuccess) return hip_fail(e, "phase1 launch");
   } else {
     elsa::Phase2Params p{};

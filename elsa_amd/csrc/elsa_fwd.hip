@@ -711,45 +711,57 @@ static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-// fp16/bf16: 64 rows per wave for head dims <= 64 (32 for 128); 1 (or 2) waves for
-// sequences of at most 64 rows, 4 waves otherwise.  fp32: 32 rows per wave.
-int phase1_rows_per_wave(int dtype, int dp) { return (dtype != ELSA_F32 && dp <= 64) ? 64 : 32; }
+// Rows per Phase-1 workgroup (block_m).  fp16/bf16 at head dims <= 64: 64 rows per wave
+// in 4 waves (256 rows); sequences of at most kSmallSeq rows use 32 rows per wave (128-row
+// workgroups: twice the workgroups, half the MFMA chain per key stage, which is what
+// bounds a launch that fits on the chip in one go); at most 64 rows, one 64-row wave.
+// Head dim 128 and fp32: 32 rows per wave, 4 waves (2 for at most 64 rows).
+// Measured on MI355X (Phase 1 + Phase 2, 256- against 128-row workgroups): B8 H3 N197
+// 11 against 8 us, B1 H8 N1024 22 against 15 us, B8 H3 N1025 25 against 24 us, B1 H8 N4096
+// 64 against 70 us, B1 H8 N16384 617 against 703 us.
+constexpr int64_t kSmallSeq = 1024;
+int phase1_block_m(int dtype, int dp, int64_t n) {
+  if (n <= 64) return 64;
+  if (dtype == ELSA_F32 || dp > 64) return 128;
+  return n <= kSmallSeq ? 128 : 256;
+}
 
 template <typename T, int DP>
-static hipError_t launch1h_wb(const Phase1Params& p, int waves, hipStream_t st) {
+static hipError_t launch1h_wb(const Phase1Params& p, int block_m, hipStream_t st) {
   const bool b = p.bias.ptr != nullptr;
   if constexpr (DP <= 64) {
-    if (waves == 1) return b ? launch1h<T, DP, 2, 1, true>(p, st) : launch1h<T, DP, 2, 1, false>(p, st);
+    if (block_m == 64) return b ? launch1h<T, DP, 2, 1, true>(p, st) : launch1h<T, DP, 2, 1, false>(p, st);
+    if (block_m == 128) return b ? launch1h<T, DP, 1, 4, true>(p, st) : launch1h<T, DP, 1, 4, false>(p, st);
     return b ? launch1h<T, DP, 2, 4, true>(p, st) : launch1h<T, DP, 2, 4, false>(p, st);
   } else {
-    if (waves == 2) return b ? launch1h<T, DP, 1, 2, true>(p, st) : launch1h<T, DP, 1, 2, false>(p, st);
+    if (block_m == 64) return b ? launch1h<T, DP, 1, 2, true>(p, st) : launch1h<T, DP, 1, 2, false>(p, st);
     return b ? launch1h<T, DP, 1, 4, true>(p, st) : launch1h<T, DP, 1, 4, false>(p, st);
   }
 }
 
 template <typename T>
-static hipError_t launch1h_d(const Phase1Params& p, int waves, hipStream_t st) {
+static hipError_t launch1h_d(const Phase1Params& p, int block_m, hipStream_t st) {
   switch (pad_head_dim(p.D)) {
-    case 32: return launch1h_wb<T, 32>(p, waves, st);
-    case 64: return launch1h_wb<T, 64>(p, waves, st);
-    default: return launch1h_wb<T, 128>(p, waves, st);
+    case 32: return launch1h_wb<T, 32>(p, block_m, st);
+    case 64: return launch1h_wb<T, 64>(p, block_m, st);
+    default: return launch1h_wb<T, 128>(p, block_m, st);
   }
 }
 
 template <int DP>
-static hipError_t launch1_f32_wb(const Phase1Params& p, int waves, hipStream_t st) {
+static hipError_t launch1_f32_wb(const Phase1Params& p, int block_m, hipStream_t st) {
   const bool b = p.bias.ptr != nullptr;
-  if (waves == 2) return b ? launch1<float, DP, 2, true>(p, st) : launch1<float, DP, 2, false>(p, st);
+  if (block_m == 64) return b ? launch1<float, DP, 2, true>(p, st) : launch1<float, DP, 2, false>(p, st);
   return b ? launch1<float, DP, 4, true>(p, st) : launch1<float, DP, 4, false>(p, st);
 }
 
-hipError_t launch_phase1(const Phase1Params& p, int dtype, int waves, hipStream_t st) {
-  if (dtype == ELSA_F16) return launch1h_d<f16>(p, waves, st);
-  if (dtype == ELSA_BF16) return launch1h_d<bf16>(p, waves, st);
+hipError_t launch_phase1(const Phase1Params& p, int dtype, int block_m, hipStream_t st) {
+  if (dtype == ELSA_F16) return launch1h_d<f16>(p, block_m, st);
+  if (dtype == ELSA_BF16) return launch1h_d<bf16>(p, block_m, st);
   switch (pad_head_dim(p.D)) {
-    case 32: return launch1_f32_wb<32>(p, waves, st);
-    case 64: return launch1_f32_wb<64>(p, waves, st);
-    default: return launch1_f32_wb<128>(p, waves, st);
+    case 32: return launch1_f32_wb<32>(p, block_m, st);
+    case 64: return launch1_f32_wb<64>(p, block_m, st);
+    default: return launch1_f32_wb<128>(p, block_m, st);
   }
 }
 

@@ -94,6 +94,15 @@ def test_plan_causal_short_sequences_keep_the_workgroup_target():
     assert rc_c == rc_n == 0 and pc.partition_len == pn.partition_len == 512
 
 
+@pytest.mark.parametrize("n,d,dtype,bm", [(49, 32, _lib.ELSA_F16, 64), (197, 64, _lib.ELSA_F16, 128),
+                                         (1024, 64, _lib.ELSA_BF16, 128), (1025, 64, _lib.ELSA_F16, 256),
+                                         (16384, 64, _lib.ELSA_F16, 256), (4096, 128, _lib.ELSA_F16, 128),
+                                         (4096, 64, _lib.ELSA_F32, 128), (64, 64, _lib.ELSA_F32, 64)])
+def test_plan_block_m_by_sequence_length(n, d, dtype, bm):
+    rc, p = _plan(_args(n=n, d=d, dtype=dtype))
+    assert rc == 0 and p.block_m == bm
+
+
 def test_plan_user_partition_and_chunk():
     rc, p = _plan(_args(n=513, bh=(1, 2), part=128, qc=128))
     assert rc == 0 and p.partition_len == 128 and p.partitions == 5 and p.q_chunk == 128
