@@ -73,7 +73,11 @@ def _canonical_bias(
     elif bias.dim() == 4:
         if bias.shape[0] not in (1, batch) or bias.shape[1] not in (1, heads):
             raise ValueError("4D bias must broadcast as [B,H,N,N]")
-        view = bias.contiguous()
+        # the kernels take any strides: a 4D bias with dense keys and no broadcast (zero-stride)
+        # dimension is used as it is, e.g. rows padded to a 16-byte multiple for vector loads
+        dense_keys = bias.stride(-1) == 1
+        no_broadcast = all(st > 0 or sz == 1 for st, sz in zip(bias.stride(), bias.shape))
+        view = bias if dense_keys and no_broadcast else bias.contiguous()
     else:
         raise ValueError("bias must have shape [N,N], [H,N,N], or [B,H,N,N]")
     if view.dtype not in (torch.float16, torch.bfloat16, torch.float32):

@@ -62,6 +62,59 @@ __device__ inline float load_bias(const BiasView& b, int bi, int hi, int row, in
   return static_cast<float>(static_cast<const bf16*>(b.ptr)[off]);
 }
 
+// Bias rows that 16-byte loads can read: 16-bit values, key stride 1, batch / head / row
+// strides in multiples of 8 elements and a 16-byte aligned base.
+__device__ inline bool bias_rows_vectorizable(const BiasView& b) {
+  return b.dtype != ELSA_F32 && b.sk == 1 && b.sq % 8 == 0 && b.sb % 8 == 0 && b.sh % 8 == 0 &&
+         reinterpret_cast<uintptr_t>(b.ptr) % 16 == 0;
+}
+
+// Bias of one query row (element offset row_off) at keys key0 + 16 j + t (j < 2, t < 8) into
+// v[8 j + t]: the keys the D-layout registers of one 32-key sub-tile hold (key_of_reg).
+// Keys at or past k_end read as 0 (the caller masks them).  vec: one 16-byte load per 8 keys.
+template <typename B16>
+__device__ inline void bias_keys16_vec(const BiasView& b, int64_t row_off, int key0, int k_end, float (&v)[16]) {
+  typedef B16 b8 __attribute__((ext_vector_type(8)));
+  const B16* base = static_cast<const B16*>(b.ptr) + row_off;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int k = key0 + 16 * j;
+    if (k + 8 <= k_end) {
+      const b8 c = *reinterpret_cast<const b8*>(base + k);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[8 * j + t] = static_cast<float>(c[t]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[8 * j + t] = k + t < k_end ? static_cast<float>(base[k + t]) : 0.f;
+    }
+  }
+}
+
+__device__ inline void bias_keys16(const BiasView& b, int64_t row_off, int key0, int k_end, bool vec, float (&v)[16]) {
+  if (vec) {
+    if (b.dtype == ELSA_F16)
+      bias_keys16_vec<f16>(b, row_off, key0, k_end, v);
+    else
+      bias_keys16_vec<bf16>(b, row_off, key0, k_end, v);
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int key = key0 + 16 * (r >> 3) + (r & 7);
+    float x = 0.f;
+    if (key < k_end) {
+      const int64_t off = row_off + (int64_t)key * b.sk;
+      if (b.dtype == ELSA_F32)
+        x = static_cast<const float*>(b.ptr)[off];
+      else if (b.dtype == ELSA_F16)
+        x = static_cast<float>(static_cast<const f16*>(b.ptr)[off]);
+      else
+        x = static_cast<float>(static_cast<const bf16*>(b.ptr)[off]);
+    }
+    v[r] = x;
+  }
+}
+
 __device__ inline void store4(void* base, int64_t off, int dtype, float a, float b, float c, float d) {
   if (dtype == ELSA_F32) {
     f32x4 v = {a, b, c, d};
@@ -429,6 +482,7 @@ void phase1_half_kernel(const Phase1Params p) {
     for (int dt = 0; dt < NDT; ++dt) oacc[rt][dt] = f32x16{};
   }
   const float cs = p.scale_log2;
+  const bool bias_vec = HAS_BIAS && bias_rows_vectorizable(p.bias);
   const int ntiles = (k_end - k_begin + KT - 1) / KT;
 
   gload(k_begin);
@@ -468,17 +522,20 @@ void phase1_half_kernel(const Phase1Params p) {
         float mx = kNegInf;
         if constexpr (HAS_BIAS) {
           const bool row_ok = my_row < q_end;
+          const int64_t roff = bi * p.bias.sb + hi * p.bias.sh + (int64_t)(row_ok ? my_row : p.q_start) * p.bias.sq;
 #pragma unroll
-          for (int sub = 0; sub < NSUB; ++sub)
+          for (int sub = 0; sub < NSUB; ++sub) {
+            float bv[16];
+            bias_keys16(p.bias, roff, t0 + sub * 32 + 8 * g, k_end, bias_vec, bv);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int key = t0 + sub * 32 + key_of_reg(r, g);
               const bool ok = row_ok && key < k_end && (!p.causal || key <= my_row);
-              const float x =
-                  ok ? fmaf(s[rt][sub][r], cs, load_bias(p.bias, bi, hi, my_row, key) * p.bias_log2) : kNegInf;
+              const float x = ok ? fmaf(s[rt][sub][r], cs, bv[r] * p.bias_log2) : kNegInf;
               s[rt][sub][r] = x;
               mx = fmaxf(mx, x);
             }
+          }
         } else {
           const bool need_mask = (t0 + KT > k_end) || (p.causal && (t0 + KT - 1 > row0 + rt * 32));
           if (need_mask) {

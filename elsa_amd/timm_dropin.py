@@ -16,6 +16,7 @@ from typing import Optional
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from .attention import _twopass_attention
 from .vision_models import relative_position_index, resize_rel_pos_bias_table
@@ -135,13 +136,52 @@ class _SwinWindowCommon(nn.Module):
         return self.qkv(x).reshape(batch_windows, seq_len, 3, self.num_heads, self.head_dim)
 
     def _bias(self, mask: Optional[torch.Tensor], batch_windows: int, seq_len: int) -> torch.Tensor:
-        bias = self._get_rel_pos_bias()
-        if mask is not None:
-            num_win = int(mask.shape[0])
-            mask_bias = mask.view(1, num_win, 1, seq_len, seq_len).expand(
-                batch_windows // num_win, -1, self.num_heads, -1, -1)
-            bias = bias + mask_bias.reshape(-1, self.num_heads, seq_len, seq_len)
-        return bias
+        """Relative-position bias plus the shifted-window mask, [B_win | 1, H, N, N].
+
+        The values are the reference's sums (timm_dropin.py:85-90).  The tensor is built with
+        rows padded to a multiple of 8 keys and returned as its [..., :N] view, so that the
+        kernels read each row's keys with 16-byte loads (inference: when the table records no
+        gradient).  The padding costs no launch: the
+        table gather uses an index whose pad columns point at a valid table row (those keys
+        are never read, and their gradient is zero), and the mask is padded once per mask."""
+        npad = (-seq_len) % 8
+        # with a gradient to the table, autograd would rebuild the padded layout in the
+        # backward (a zero fill and a copy per layer): training keeps the dense bias
+        needs_grad = torch.is_grad_enabled() and self.relative_position_bias_table.requires_grad
+        if npad == 0 or needs_grad:
+            bias = self._get_rel_pos_bias()
+            if mask is not None:
+                num_win = int(mask.shape[0])
+                mask_bias = mask.view(1, num_win, 1, seq_len, seq_len).expand(
+                    batch_windows // num_win, -1, self.num_heads, -1, -1)
+                bias = bias + mask_bias.reshape(-1, self.num_heads, seq_len, seq_len)
+            return bias
+        width, h = seq_len + npad, self.num_heads
+        rel = self.relative_position_bias_table[self._padded_index(seq_len, npad)]
+        rel = rel.view(seq_len, width, h).permute(2, 0, 1).contiguous().unsqueeze(0)
+        if mask is None:
+            return rel[..., :seq_len]
+        num_win = int(mask.shape[0])
+        m = self._padded_mask(mask, npad)
+        bias = rel.view(1, 1, h, seq_len, width) + m.view(1, num_win, 1, seq_len, width)
+        bias = bias.expand(batch_windows // num_win, -1, -1, -1, -1).reshape(-1, h, seq_len, width)
+        return bias[..., :seq_len]
+
+    def _padded_index(self, seq_len: int, npad: int) -> torch.Tensor:
+        idx = self.relative_position_index
+        key = (idx.data_ptr(), tuple(idx.shape), idx.device, npad)
+        cached = self.__dict__.get("_elsa_index_cache")
+        if cached is None or cached[0] != key:
+            padded = F.pad(idx.reshape(seq_len, seq_len), (0, npad)).reshape(-1)  # pads with index 0
+            self.__dict__["_elsa_index_cache"] = (key, padded)
+        return self.__dict__["_elsa_index_cache"][1]
+
+    def _padded_mask(self, mask: torch.Tensor, npad: int) -> torch.Tensor:
+        key = (mask.data_ptr(), tuple(mask.shape), mask.dtype, mask.device, mask._version, npad)
+        cached = self.__dict__.get("_elsa_mask_cache")
+        if cached is None or cached[0] != key:
+            self.__dict__["_elsa_mask_cache"] = (key, F.pad(mask, (0, npad)))
+        return self.__dict__["_elsa_mask_cache"][1]
 
     def _qkv_and_bias(self, x: torch.Tensor, mask: Optional[torch.Tensor]):
         batch_windows, seq_len, _ = x.shape

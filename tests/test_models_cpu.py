@@ -101,3 +101,33 @@ def test_model_pairs_share_weights():
     assert base(x).shape == (1, 16, 96) and tb(x).shape == (1, 16, 96)
     with pytest.raises(ValueError, match="divisible"):
         elsa_amd.make_model_pair(dim=95, heads=3)
+
+
+def test_swin_bias_values_and_padded_row_layout():
+    """The drop-in's window bias equals the reference's rel-pos bias + shifted-window mask, and
+    its rows are padded to a multiple of 8 keys (a 16-byte aligned row stride in fp16)."""
+    torch.manual_seed(3)
+    m = swin_tiny_patch4_window7(224)
+    elsa_amd.patch_timm_attention(m)
+    blk = m.layers[0].blocks[1]  # a shifted block: it has a mask
+    attn, mask = blk.attn, blk.attn_mask
+    assert mask is not None
+    n, nw, h = attn.window_area, mask.shape[0], attn.num_heads
+    b_win = 2 * nw
+    with torch.no_grad():
+        bias = attn._bias(mask, b_win, n)
+        plain = attn._bias(None, b_win, n)
+    dense = attn._bias(mask, b_win, n)  # the table records a gradient: dense rows
+    assert dense.is_contiguous() and torch.equal(dense, bias)
+    rel = attn._get_rel_pos_bias().detach()
+    ref = rel + mask.view(1, nw, 1, n, n).expand(b_win // nw, -1, h, -1, -1).reshape(-1, h, n, n)
+    assert bias.shape == (b_win, h, n, n) and torch.equal(bias, ref)
+    assert bias.stride(-1) == 1 and bias.stride(-2) % 8 == 0 and bias.stride(-2) >= n
+    assert plain.shape == (1, h, n, n) and torch.equal(plain, rel) and plain.stride(-2) % 8 == 0
+    # the canonical view keeps that layout (no copy)
+    from elsa_amd.attention import _canonical_bias
+
+    meta = _canonical_bias(bias, batch=b_win, heads=h, seq_len=n, device=bias.device)
+    assert meta.tensor.data_ptr() == bias.data_ptr() and meta.stride_q == bias.stride(-2)
+    broadcast = rel.expand(b_win, -1, -1, -1)  # a zero batch stride is still materialised
+    assert _canonical_bias(broadcast, batch=b_win, heads=h, seq_len=n, device=rel.device).stride_b == h * n * n
