@@ -179,16 +179,16 @@ __device__ inline WgCoord xcd_order() {
   return {l % gx, (l / gx) % gy, l / (gx * gy)};
 }
 // Phase 1 order (grid x = row block, y = head, z = K partition).  Non-causal: the XCD
-// order with z varying fastest, so one XCD's range covers all partitions of consecutive
-// row blocks of one head and the row block's Q tile is shared in L2 by its partitions.
-// Causal: the work of a row block grows with its index and vanishes for partitions past
-// it; there the dispatcher's own round-robin over XCDs balances best, with the row blocks
-// reversed so that the heaviest start first.
+// order (row blocks fastest), so the workgroups resident on one XCD share one K/V
+// partition panel in its L2: Phase 1 then fetches its algorithmic bytes (Q once per
+// partition, K and V once; 101 MB at B1 H8 N16K d64 with 4 partitions), where a
+// partition-fastest order fetched 244 MB in the same time.  Causal: the work of a row block
+// grows with its index and vanishes for partitions past it; there the dispatcher's own
+// round-robin over XCDs balances best, with the row blocks reversed so that the heaviest
+// start first.
 __device__ inline WgCoord phase1_order(bool causal) {
-  const int gx = gridDim.x, gz = gridDim.z;
-  if (causal) return {gx - 1 - (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
-  const int l = xcd_linear(), rest = l / gz;
-  return {rest % gx, rest / gx, l % gz};
+  if (causal) return {(int)gridDim.x - 1 - (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
+  return xcd_order();
 }
 
 // Combine the two 32-lane halves of a wave (lanes l and l ^ 32) with
