@@ -179,6 +179,12 @@ int run_phase(const elsa_fwd_args* a, const elsa_fwd_plan& pl, int q_start, int 
     p.causal = a->is_causal ? 1 : 0;
     p.scale_log2 = (float)(1.4426950408889634 * softmax_scale(a->scale, a->head_dim));
     p.bias_log2 = 1.4426950408889634f;
+    // the reference's d64 fast path (attention_parallel_scan.py:418-440, :983-1018): fp16 without
+    // bias or causal mask, a user block_n that is a multiple of 64, summaries in the input dtype
+    p.prescale_q = (a->dtype == ELSA_F16 && a->head_dim == 64 && !p.bias.ptr && !a->is_causal &&
+                    a->summary_dtype == a->dtype && a->partition_len % 64 == 0)
+                       ? 1
+                       : 0;
     p.rows_pad = pl.q_chunk;
     hipError_t e = elsa::launch_phase1(p, a->dtype, pl.block_m, st);
     if (e != hipSuccess) return hip_fail(e, "phase1 launch");

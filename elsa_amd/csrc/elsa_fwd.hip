@@ -378,13 +378,20 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
 // exceeds it by more than kLazyTau (p stays <= 2^kLazyTau, exact in fp16/bf16 and
 // fp32), and the summary is renormalised to the exact row maximum at the end.
 // The row sum accumulates the fp32 p values; the MFMA takes them rounded to T.
+//
+// PRE (prescale_q): q is rounded to T after scaling by scale*log2(e), as the reference's fp16
+// d64 fold does, so the QK^T product yields base-2 scores.  The product then starts from
+// -m_run (the MFMA's accumulator input, a register set refreshed only when the lazy max
+// moves), so its output is already score - m_run and p = exp2 of it, with no per-score
+// scale-and-subtract.
 constexpr float kLazyTau = 8.0f;
 
 // 2 waves per SIMD, except the 1- and 2-wave variants at D >= 64 (sequences of at most 64
 // keys): their register staging of a whole 64-key stage does not fit that budget.
-template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS>
+template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS, bool PRE>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu((WAVES <= 2 && DP >= 64) ? 1 : 2, 2)))
 void phase1_half_kernel(const Phase1Params p) {
+  static_assert(!(PRE && HAS_BIAS), "the prescaled fold has no bias");
   using M = Mfma<T>;
   typedef typename M::frag F;
   constexpr int KT = 64;          // keys per LDS stage
@@ -429,6 +436,10 @@ void phase1_half_kernel(const Phase1Params p) {
     for (int kk = 0; kk < NKK; ++kk) {
       const int d0 = kk * 16 + g * 8;
       qf[rt][kk] = load_frag<T>(Q + (int64_t)(ok ? row : 0) * p.qs[2] + d0, ok && d0 < p.D);
+      if constexpr (PRE) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) qf[rt][kk][t] = static_cast<T>(static_cast<float>(qf[rt][kk][t]) * p.scale_log2);
+      }
     }
   }
 
@@ -484,6 +495,10 @@ void phase1_half_kernel(const Phase1Params p) {
   const float cs = p.scale_log2;
   const bool bias_vec = HAS_BIAS && bias_rows_vectorizable(p.bias);
   const int ntiles = (k_end - k_begin + KT - 1) / KT;
+  // PRE: accumulator input of the QK^T product, -ref with ref = m_run (0 while m_run = -inf)
+  f32x16 negref[PRE ? RT : 1];
+#pragma unroll
+  for (int rt = 0; rt < (PRE ? RT : 1); ++rt) negref[rt] = f32x16{};
 
   gload(k_begin);
   sstore(0);
@@ -508,9 +523,9 @@ void phase1_half_kernel(const Phase1Params p) {
         for (int kk = 0; kk < NKK; ++kk) kf[kk] = *reinterpret_cast<const F*>(krow + kk * 16);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-          s[rt][sub] = f32x16{};
+          s[rt][sub] = M::mma(kf[0], qf[rt][0], PRE ? negref[PRE ? rt : 0] : f32x16{});
 #pragma unroll
-          for (int kk = 0; kk < NKK; ++kk) s[rt][sub] = M::mma(kf[kk], qf[rt][kk], s[rt][sub]);
+          for (int kk = 1; kk < NKK; ++kk) s[rt][sub] = M::mma(kf[kk], qf[rt][kk], s[rt][sub]);
         }
       }
 
@@ -558,7 +573,11 @@ void phase1_half_kernel(const Phase1Params p) {
           mx = fmaxf(mx, mx1);
         }
         mx = wave_max_pair(mx);
-        m_tile[rt] = HAS_BIAS ? mx : mx * cs;
+        if constexpr (PRE) {
+          m_tile[rt] = mx - negref[rt][0];  // the product started from -ref
+        } else {
+          m_tile[rt] = HAS_BIAS ? mx : mx * cs;
+        }
         m_true[rt] = fmaxf(m_true[rt], m_tile[rt]);
         raise |= m_tile[rt] > m_run[rt] + kLazyTau;
       }
@@ -573,6 +592,18 @@ void phase1_half_kernel(const Phase1Params p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) oacc[rt][dt][r] *= alpha;
           m_run[rt] = m_new;
+          if constexpr (PRE) {
+            // the scores are relative to the old reference: move them to the new one (a row
+            // still at -inf has only -inf scores and keeps reference 0)
+            const float ref = (m_new == kNegInf) ? 0.f : m_new;
+            const float shift = ref + negref[rt][0];
+#pragma unroll
+            for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) s[rt][sub][r] -= shift;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) negref[rt][r] = -ref;
+          }
         }
       }
 
@@ -585,7 +616,12 @@ void phase1_half_kernel(const Phase1Params p) {
         for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const float pr = HAS_BIAS ? fast_exp2(s[rt][sub][r] + nm) : fast_exp2(fmaf(s[rt][sub][r], cs, nm));
+            float pr;
+            if constexpr (PRE) {
+              pr = fast_exp2(s[rt][sub][r]);
+            } else {
+              pr = HAS_BIAS ? fast_exp2(s[rt][sub][r] + nm) : fast_exp2(fmaf(s[rt][sub][r], cs, nm));
+            }
             s[rt][sub][r] = pr;
             zs += pr;
           }
@@ -764,7 +800,13 @@ template <typename T, int DP, int RT, int W, bool B>
 static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
   constexpr int BM = 32 * RT * W;
   const dim3 grid((p.q_len + BM - 1) / BM, p.BH, p.P);
-  hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, B>), grid, dim3(64 * W), 0, st, p);
+  if constexpr (!B && DP == 64 && std::is_same<T, f16>::value) {
+    if (p.prescale_q) {
+      hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, false, true>), grid, dim3(64 * W), 0, st, p);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, B, false>), grid, dim3(64 * W), 0, st, p);
   return hipGetLastError();
 }
 

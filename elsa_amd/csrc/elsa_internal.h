@@ -34,6 +34,10 @@ struct Phase1Params {
   int causal;
   float scale_log2;  // log2(e) / sqrt(D_model)
   float bias_log2;   // log2(e)
+  // q rounded to the input dtype after scaling by scale_log2, so the scores come out of the
+  // QK^T product in the base-2 domain (the reference's fp16 d64 fold without bias or
+  // causal mask, attention_parallel_scan.py:257-259); otherwise fp32 scores are scaled
+  int prescale_q;
   int64_t rows_pad;
   // direct != 0 (only with P == 1): apply Phase 2's finalize in the epilogue and write
   // out (the input dtype, layout os) and the row state instead of the summary

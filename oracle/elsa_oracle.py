@@ -351,13 +351,17 @@ def forward(
     if rows is None:
         rows = np.arange(n)
     rows = np.asarray(rows)
+    # the d64 fast path (pre-scaled q) only under _can_use_d64_parallel_final's conditions
+    # (attention_parallel_scan.py:418-440) and without a causal mask (:983-1018)
+    generic = not (bb is None and not is_causal and d == 64 and dtype in ("fp16", "fp32")
+                   and summary_dtype == dtype and (part_len is None or part_len % 64 == 0))
     if part_len is None:
         part_len = n
     parts = []
     for k0 in range(0, n, part_len):
         m, z, s = phase1_partition(
             qf[:, rows], kf, vf, row_idx=rows, k_begin=k0, k_end=min(n, k0 + part_len), n_ctx=n,
-            is_causal=is_causal, bias=bb, dtype=dtype, mode=mode, micro=micro,
+            is_causal=is_causal, bias=bb, dtype=dtype, mode=mode, micro=micro, generic=generic,
         )
         parts.append((m, z, _summary_round(s, summary_dtype, mode)))
     if merge_kind == "tree":

@@ -65,12 +65,17 @@ def test_forward_matches_oracle_and_closed_form(case):
     torch.cuda.synchronize()
     qf, kf, vf = (np.asarray(x, np.float32) for x in (q, k, v))
     eo, em, ez = O.exact_forward(qf, kf, vf, is_causal=causal)
-    ro, _, _ = O.forward(q, k, v, is_causal=causal, part_len=bn, dtype=dt, mode="ref")
+    ro, rm, _ = O.forward(q, k, v, is_causal=causal, part_len=bn, dtype=dt, mode="ref")
     describe(str(assert_parity(host(out), eo, ro, FWD_TOL[dt], "out", dt)))
     m = host(row_m)
     assert np.array_equal(np.isneginf(m), np.isneginf(em))
     fin = np.isfinite(em)
-    assert np.abs(m[fin] - em[fin]).max() <= 1e-4 * max(1.0, np.abs(em[fin]).max())
+    # the reference's fp16 d64 fold scores q rounded to fp16 after scaling
+    # (attention_parallel_scan.py:257-259), which moves its row max off the exact one by up
+    # to ~1e-3; the row max must match the reference path and stay within twice its error
+    mbar = 1e-4 * max(1.0, np.abs(em[fin]).max())
+    assert np.abs(m[fin] - rm[fin]).max() <= mbar
+    assert np.abs(m[fin] - em[fin]).max() <= max(mbar, 2 * np.abs(rm[fin] - em[fin]).max())
     np.testing.assert_allclose(host(row_z), ez, rtol=2e-3 if dt != "fp32" else 1e-5)
 
 
@@ -158,14 +163,15 @@ def test_two_pass_structure(causal):
     out, rm, rz, m_buf, z_buf, s_buf, plan = two_pass_explicit(dev(q, "fp16"), dev(k, "fp16"), dev(v, "fp16"),
                                                                  is_causal=causal, block_n=256)
     assert plan["partitions"] == 4 and tuple(s_buf.shape) == (4, 2, 1000, 64)
-    # every partition summary equals the oracle's fold of that partition
+    # every partition summary equals the oracle's fold of that partition at the reference's
+    # rounding points (non-causal fp16 d64: q rounded after scaling, attention_parallel_scan.py:257-259)
     qf = np.float32(q).reshape(2, 1000, 64)
     for kb in range(4):
         rows = np.arange(1000) if not causal else np.arange(kb * 256, 1000)
         pm, pz, ps = O.phase1_partition(qf[:, rows], np.float32(k).reshape(2, 1000, 64),
                                         np.float32(v).reshape(2, 1000, 64), row_idx=rows, k_begin=kb * 256,
                                         k_end=min(1000, kb * 256 + 256), n_ctx=1000, is_causal=causal, bias=None,
-                                        dtype="fp32", mode="fp64")
+                                        dtype="fp16", mode="ref")
         hm = host(m_buf[kb])[:, rows]
         assert np.abs(hm - pm).max() < 1e-4
         np.testing.assert_allclose(host(z_buf[kb])[:, rows], pz, rtol=2e-3)
