@@ -444,6 +444,15 @@ void bwd_dq_half_kernel(const BwdParams p) {
     live[rt] = ok && lse[rt] < __builtin_huge_valf();
   }
   const int k_end = p.causal ? wg_last + 1 : p.N;
+  // -D of this lane's row: the dP^T product starts from it and yields dP - D directly.  The
+  // 16 registers of that constant would spill in the bias and D = 128 variants, which
+  // subtract D from each score instead.
+  constexpr bool SEED_D = !HAS_BIAS && DP <= 64;
+  f32x16 ndd[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ndd[rt][r] = SEED_D ? -dd[rt] : 0.f;
 
   // element offsets of this thread's staging chunks inside a stage (row strides are
   // below 2^25 elements, checked by the API, so 64 rows fit in 32 bits)
@@ -513,9 +522,9 @@ static_for<0, NCH>([&](auto I) {
         f32x16 ds[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-          f32x16 s = f32x16{}, dp = f32x16{};
+          f32x16 s = M::mma(kf[0], qf[rt][0], f32x16{}), dp = M::mma(vf[0], gf[rt][0], ndd[rt]);
 #pragma unroll
-          for (int kk = 0; kk < NKK; ++kk) {
+          for (int kk = 1; kk < NKK; ++kk) {
             s = M::mma(kf[kk], qf[rt][kk], s);
             dp = M::mma(vf[kk], gf[rt][kk], dp);
           }
@@ -543,7 +552,7 @@ static_for<0, NCH>([&](auto I) {
               }
             }
 #pragma unroll
-            for (int r = 0; r < 16; ++r) ds[rt][r] *= dp[r] - dd[rt];
+            for (int r = 0; r < 16; ++r) ds[rt][r] *= SEED_D ? dp[r] : dp[r] - dd[rt];
           }
         }
 #pragma unroll
@@ -601,7 +610,7 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) T Qs[2][RTS * KS];
   __shared__ __attribute__((aligned(16))) T Gs[2][RTS * KS];
   __shared__ __attribute__((aligned(16))) float lse_s[2][RTS];
-  __shared__ __attribute__((aligned(16))) float dd_s[2][RTS];
+  __shared__ __attribute__((aligned(16))) float ndd_s[2][RTS];  // -D of the stage's rows
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
@@ -670,7 +679,7 @@ static_for<0, NCH>([&](auto I) {
     if (tid < RTS) {  // rows past N: LSE2 = +inf makes their p exactly 0
       const int ra = t0 + tid;
       lreg = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : __builtin_huge_valf();
-      dreg = ra < p.N ? p.d_row[(int64_t)bh * p.N + ra] : 0.f;
+      dreg = ra < p.N ? -p.d_row[(int64_t)bh * p.N + ra] : 0.f;
     }
   };
   auto sstore = [&](int buf) {
@@ -683,7 +692,7 @@ static_for<0, NCH>([&](auto I) {
     });
     if (tid < RTS) {
       lse_s[buf][tid] = lreg;
-      dd_s[buf][tid] = dreg;
+      ndd_s[buf][tid] = dreg;
     }
   };
 
@@ -719,11 +728,24 @@ static_for<0, NCH>([&](auto I) {
             gta[j][dt] = tr_frag<T>(gs + (sub * 32 + 16 * j + tr_row) * KS, KS, dt * 32 + tr_col);
             qta[j][dt] = tr_frag<T>(qs + (sub * 32 + 16 * j + tr_row) * KS, KS, dt * 32 + tr_col);
           }
+        // -D of the rows of registers 8j..8j+7 (sub*32 + 16j + 8g + t): the dP^T product starts
+        // from it and yields dP - D directly
+        f32x16 ndd;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float* e8 = &ndd_s[buf][sub * 32 + 16 * j + 8 * g];
+          const f32x4 e0 = *reinterpret_cast<const f32x4*>(e8), e1 = *reinterpret_cast<const f32x4*>(e8 + 4);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            ndd[8 * j + t] = e0[t];
+            ndd[8 * j + 4 + t] = e1[t];
+          }
+        }
 #pragma unroll
         for (int kt = 0; kt < KRT; ++kt) {
-          f32x16 s = f32x16{}, dp = f32x16{};
+          f32x16 s = M::mma(qa[0], kf[kt][0], f32x16{}), dp = M::mma(ga[0], vf[kt][0], ndd);
 #pragma unroll
-          for (int kk = 0; kk < NKK; ++kk) {
+          for (int kk = 1; kk < NKK; ++kk) {
             s = M::mma(qa[kk], kf[kt][kk], s);
             dp = M::mma(ga[kk], vf[kt][kk], dp);
           }
@@ -733,9 +755,7 @@ static_for<0, NCH>([&](auto I) {
           for (int j = 0; j < 2; ++j) {
             // rows of registers 8j..8j+7: sub*32 + 16j + 8g + t (consecutive)
             const float* lp = &lse_s[buf][sub * 32 + 16 * j + 8 * g];
-            const float* dq8 = &dd_s[buf][sub * 32 + 16 * j + 8 * g];
             const f32x4 l0 = *reinterpret_cast<const f32x4*>(lp), l1 = *reinterpret_cast<const f32x4*>(lp + 4);
-            const f32x4 e0 = *reinterpret_cast<const f32x4*>(dq8), e1 = *reinterpret_cast<const f32x4*>(dq8 + 4);
             float pr[8];
             if constexpr (HAS_BIAS) {
 #pragma unroll
@@ -762,7 +782,7 @@ static_for<0, NCH>([&](auto I) {
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
               bp[t] = static_cast<T>(pr[t]);
-              bs[t] = static_cast<T>(pr[t] * (dp[8 * j + t] - (t < 4 ? e0[t] : e1[t - 4])));
+              bs[t] = static_cast<T>(pr[t] * dp[8 * j + t]);
             }
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
