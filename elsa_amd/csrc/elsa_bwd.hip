@@ -177,7 +177,8 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
-  const WgCoord wg = xcd_order();
+  WgCoord wg = xcd_order();
+  if (p.causal) wg.x = (int)gridDim.x - 1 - wg.x;  // causal: heaviest row blocks first
   const int bh = wg.y;
   const int wg_row0 = wg.x * BM;
   const int wg_last = min(p.N, wg_row0 + BM) - 1;
@@ -412,7 +413,10 @@ void bwd_dq_half_kernel(const BwdParams p) {
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
-  const WgCoord wg = xcd_order();
+  // causal: the work of a row block grows with its index; each XCD takes its range of
+  // row blocks heaviest first
+  WgCoord wg = xcd_order();
+  if (p.causal) wg.x = (int)gridDim.x - 1 - wg.x;
   const int bh = wg.y;
   const int wg_row0 = wg.x * BM;
   const int wg_last = min(p.N, wg_row0 + BM) - 1;
@@ -831,7 +835,8 @@ __global__ __launch_bounds__(64 * WAVES) void row_stats_kernel(const BwdParams p
   __shared__ __attribute__((aligned(16))) T Kt[C::HALF ? 1 : DP * C::TS];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
-  const WgCoord wg = xcd_order();
+  WgCoord wg = xcd_order();
+  if (p.causal) wg.x = (int)gridDim.x - 1 - wg.x;  // causal: heaviest row blocks first
   const int bh = wg.y;
   const int wg_row0 = wg.x * BM;
   const int wg_last = min(p.N, wg_row0 + BM) - 1;
