@@ -256,8 +256,13 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
 
 // ------------------------------------------------------------------ dk / dv
 // fp32 only (the fp16 / bf16 kernels follow below).
-template <typename T, int DP, int WAVES, bool HAS_BIAS>
-__global__ __launch_bounds__(64 * WAVES) void bwd_dkdv_kernel(const BwdParams p) {
+// OCC = waves per SIMD the register budget is sized for.  At 2 (D <= 64) the kernel fits 250
+// VGPRs but has no registers left to read LDS operands ahead; a second resident wave hides
+// that when the grid has two work-groups per CU (B1 H8 d64: 16K 11.84 -> 10.95 ms), while a
+// grid of one work-group per CU runs faster at 1 (4K 0.761 against 0.965 ms).
+template <typename T, int DP, int WAVES, bool HAS_BIAS, int OCC>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(OCC, 2)))
+void bwd_dkdv_kernel(const BwdParams p) {
   static_assert(sizeof(T) == 4, "fp32 kernel");
   using C = BwdCfg<T, DP>;
   using M = Mfma<T>;
@@ -996,7 +1001,10 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (stage < 0 || stage == 2) {
-      hipLaunchKernelGGL((bwd_dkdv_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
+      if (DP <= 64 && (int64_t)grid.x * grid.y >= 2 * 256)
+        hipLaunchKernelGGL((bwd_dkdv_kernel<T, DP, W, B, 2>), grid, dim3(64 * W), 0, st, p);
+      else
+        hipLaunchKernelGGL((bwd_dkdv_kernel<T, DP, W, B, 1>), grid, dim3(64 * W), 0, st, p);
       e = hipGetLastError();
     }
   }
