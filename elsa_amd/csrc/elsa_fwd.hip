@@ -835,7 +835,10 @@ template <typename T, int DP>
 static hipError_t launch1h_wb(const Phase1Params& p, int block_m, hipStream_t st) {
   const bool b = p.bias.ptr != nullptr;
   if constexpr (DP <= 64) {
-    if (block_m == 64) return b ? launch1h<T, DP, 2, 1, true>(p, st) : launch1h<T, DP, 2, 1, false>(p, st);
+    // 64 rows with a bias: two waves of 32 rows.  One wave of 64 rows holds the bias values of
+    // both row tiles and spilled 148 bytes per lane at D = 32 (Swin-T's 49-token windows: its
+    // 224 px forward 1.531 -> 1.469 ms, 512 px 4.371 -> 4.253 ms).
+    if (block_m == 64) return b ? launch1h<T, DP, 1, 2, true>(p, st) : launch1h<T, DP, 2, 1, false>(p, st);
     if (block_m == 128) return b ? launch1h<T, DP, 1, 4, true>(p, st) : launch1h<T, DP, 1, 4, false>(p, st);
     return b ? launch1h<T, DP, 2, 4, true>(p, st) : launch1h<T, DP, 2, 4, false>(p, st);
   } else {
