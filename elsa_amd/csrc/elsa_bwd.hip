@@ -128,6 +128,25 @@ __device__ inline void f32_stage_store(const Chunk16 (&reg)[NR], float* tr, int 
   });
 }
 
+// fp32 dk/dv staging: the same register chunks written transposed with a 16-byte aligned
+// row stride TS4 (four consecutive stage rows of one d in one 16-byte load) and row-major
+// with stride RS4 (four consecutive d of one row in one 16-byte load).
+template <int DP, int NT, int NR, int TS4, int RS4>
+__device__ inline void f32_stage_store2(const Chunk16 (&reg)[NR], float* tr, float* rm, int tid) {
+  using S = F32Stage<DP, NT>;
+  static_assert(NR == S::NCH, "one register chunk per staged chunk of this thread");
+  static_for<0, S::NCH>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    const int ci = tid + i * NT;
+    if (S::TOTAL % NT == 0 || ci < S::TOTAL) {
+      const int r = ci / S::CPR, d0 = (ci % S::CPR) * 4;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) tr[(d0 + t) * TS4 + r] = __uint_as_float(reg[i][t]);
+      *reinterpret_cast<Chunk16*>(rm + r * RS4 + d0) = reg[i];
+    }
+  });
+}
+
 // ------------------------------------------------------------------ preprocess
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdParams p) {
@@ -164,16 +183,24 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdParams p) {
 }
 
 // ------------------------------------------------------------------ dq
+// fp32 only (the fp16 / bf16 kernel follows below).  The fp32 MFMA takes one operand
+// element per lane and k-step; the contraction orders are chosen so that one 16-byte LDS
+// load gives a lane four k-steps: over d, k-step kk = 4m + u of lane group g takes
+// d = 8m + 4g + u (row-major K and V tiles); over the stage keys, k-step j = 4jb + u takes
+// key key_of_reg(j, g), four consecutive keys for consecutive u (transposed K tile).
 template <typename T, int DP, int WAVES, bool HAS_BIAS>
 __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
+  static_assert(sizeof(T) == 4, "fp32 kernel");
   using C = BwdCfg<T, DP>;
   using M = Mfma<T>;
-  typedef typename M::frag F;
   constexpr int NT = 64 * WAVES, BM = 32 * WAVES;
-  __shared__ __attribute__((aligned(16))) T Ks[C::HALF ? C::TT * C::RS : 1];
-  __shared__ __attribute__((aligned(16))) T Vs[C::HALF ? C::TT * C::RS : 1];
-  __shared__ __attribute__((aligned(16))) T Kt[DP * C::TS];
-  __shared__ __attribute__((aligned(16))) T Vt[C::HALF ? 1 : DP * C::TS];
+  constexpr int TT = C::TT;       // keys per stage
+  constexpr int TS4 = TT + 4;     // transposed K tile [DP][TS4]
+  constexpr int RS4 = DP + 4;     // row-major K and V tiles [TT][RS4]
+  constexpr int NM = DP / 8;
+  __shared__ __attribute__((aligned(16))) float Kr[TT * RS4];
+  __shared__ __attribute__((aligned(16))) float Vr[TT * RS4];
+  __shared__ __attribute__((aligned(16))) float Kt[DP * TS4];
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
@@ -190,13 +217,15 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
   const T* V = static_cast<const T*>(p.v) + bi * p.vs[0] + hi * p.vs[1];
   const T* dO = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1];
 
-  F qf[C::NKK], gf[C::NKK];
+  // this lane's row of Q and dO at d = 8m + 4g .. + 3 (the B operands of S and dP)
+  f32x4 qf[NM], gf[NM];
   const int rsafe = row_ok ? my_row : 0;
 #pragma unroll
-  for (int kk = 0; kk < C::NKK; ++kk) {
-    const int d0 = kk * C::KSTEP + g * C::KP;
-    qf[kk] = load_frag<T>(Q + (int64_t)rsafe * p.qs[2] + d0, row_ok && d0 < p.D);
-    gf[kk] = load_frag<T>(dO + (int64_t)rsafe * p.gs[2] + d0, row_ok && d0 < p.D);
+  for (int m = 0; m < NM; ++m) {
+    const int d0 = 8 * m + 4 * g;
+    const bool ok = row_ok && d0 < p.D;
+    qf[m] = ok ? *reinterpret_cast<const f32x4*>(Q + (int64_t)rsafe * p.qs[2] + d0) : f32x4{};
+    gf[m] = ok ? *reinterpret_cast<const f32x4*>(dO + (int64_t)rsafe * p.gs[2] + d0) : f32x4{};
   }
   const float lse = row_ok ? p.lse_row[(int64_t)bh * p.N + my_row] : 0.f;
   const float dd = row_ok ? p.d_row[(int64_t)bh * p.N + my_row] : 0.f;
@@ -206,19 +235,40 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt) acc[dt] = f32x16{};
   const int k_end = p.causal ? wg_last + 1 : p.N;
+  constexpr int CPR = DP / 4;  // 16-byte chunks per key row
 
-  for (int t0 = 0; t0 < k_end; t0 += C::TT) {
+  for (int t0 = 0; t0 < k_end; t0 += TT) {
     __syncthreads();
-    stage_tile<T, DP, NT, C::HALF, true>(K, p.ks[2], t0, k_end, p.D, Ks, Kt, tid);
-    stage_tile<T, DP, NT, C::HALF, !C::HALF>(V, p.vs[2], t0, k_end, p.D, Vs, Vt, tid);
+    for (int ci = tid; ci < TT * CPR; ci += NT) {  // keys >= k_end and d >= D are zeros
+      const int r = ci / CPR, d0 = (ci % CPR) * 4, key = t0 + r;
+      f32x4 kv{}, vv{};
+      if (key < k_end && d0 < p.D) {
+        kv = *reinterpret_cast<const f32x4*>(K + (int64_t)key * p.ks[2] + d0);
+        vv = *reinterpret_cast<const f32x4*>(V + (int64_t)key * p.vs[2] + d0);
+      }
+      *reinterpret_cast<f32x4*>(&Kr[r * RS4 + d0]) = kv;
+      *reinterpret_cast<f32x4*>(&Vr[r * RS4 + d0]) = vv;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) Kt[(d0 + u) * TS4 + r] = kv[u];
+    }
     __syncthreads();
     f32x16 s = f32x16{}, dp = f32x16{};
+    {
+      // A operands: stage key swap23(c), d = 8m + 4g .. + 3
+      const float* kr = Kr + swap23(c) * RS4 + 4 * g;
+      const float* vr = Vr + swap23(c) * RS4 + 4 * g;
 #pragma unroll
-    for (int kk = 0; kk < C::NKK; ++kk) {
-      s = M::mma(a_frag<T, DP>(Ks, Kt, c, g, kk), qf[kk], s);
-      dp = M::mma(a_frag<T, DP>(Vs, Vt, c, g, kk), gf[kk], dp);
+      for (int m = 0; m < NM; ++m) {
+        const f32x4 ka = *reinterpret_cast<const f32x4*>(kr + 8 * m);
+        const f32x4 va = *reinterpret_cast<const f32x4*>(vr + 8 * m);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          s = M::mma(ka[u], qf[m][u], s);
+          dp = M::mma(va[u], gf[m][u], dp);
+        }
+      }
     }
-    const bool full = !HAS_BIAS && (t0 + C::TT <= k_end) && (!p.causal || t0 + C::TT - 1 <= wg_row0 + wave * 32);
+    const bool full = !HAS_BIAS && (t0 + TT <= k_end) && (!p.causal || t0 + TT - 1 <= wg_row0 + wave * 32);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = t0 + key_of_reg(r, g);
@@ -230,17 +280,14 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
       s[r] = pr * (dp[r] - dd);
     }
 #pragma unroll
-    for (int j = 0; j < C::NJ; ++j) {
-      F b;
-      if constexpr (C::KP == 1) {
-        b = s[j];
-      } else {
+    for (int jb = 0; jb < 4; ++jb) {
+      const int k0 = 16 * (jb >> 1) + 8 * g + 4 * (jb & 1);  // key_of_reg(4 jb, g)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) b[t] = static_cast<T>(s[j * 8 + t]);
+      for (int dt = 0; dt < C::NDT; ++dt) {
+        const f32x4 ka = *reinterpret_cast<const f32x4*>(Kt + (dt * 32 + c) * TS4 + k0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[dt] = M::mma(ka[u], s[4 * jb + u], acc[dt]);
       }
-#pragma unroll
-      for (int dt = 0; dt < C::NDT; ++dt)
-        acc[dt] = M::mma(load_frag<T>(Kt + (dt * 32 + c) * C::TS + key_of_reg(j * C::KP, g), true), b, acc[dt]);
     }
   }
   if (!row_ok) return;
@@ -256,21 +303,29 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
 
 // ------------------------------------------------------------------ dk / dv
 // fp32 only (the fp16 / bf16 kernels follow below).
-// OCC = waves per SIMD the register budget is sized for.  At 2 (D <= 64) the kernel fits 250
-// VGPRs but has no registers left to read LDS operands ahead; a second resident wave hides
-// that when the grid has two work-groups per CU (B1 H8 d64: 16K 11.84 -> 10.95 ms), while a
-// grid of one work-group per CU runs faster at 1 (4K 0.761 against 0.965 ms).
-template <typename T, int DP, int WAVES, bool HAS_BIAS, int OCC>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(OCC, 2)))
+// 2 waves per SIMD up to D = 64 (243 VGPRs, no AGPRs, no spills).  With one 16-byte LDS load
+// per four k-steps the waves keep their operand reads ahead of the MFMAs (B1 H8 d64: 16K
+// 10.92 -> 9.23 ms, 4K 0.764 -> 0.703 ms against one 4-byte load per k-step).
+template <typename T, int DP, int WAVES, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(DP >= 128 ? 1 : 2, 2)))
 void bwd_dkdv_kernel(const BwdParams p) {
   static_assert(sizeof(T) == 4, "fp32 kernel");
   using C = BwdCfg<T, DP>;
   using M = Mfma<T>;
-  typedef typename M::frag F;
   constexpr int NT = 64 * WAVES, BN = 32 * WAVES;
-  __shared__ __attribute__((aligned(16))) T Qt[2][DP * C::TS];
-  __shared__ __attribute__((aligned(16))) T Gt[2][DP * C::TS];
-  __shared__ float lse_s[2][C::TT], dd_s[2][C::TT];
+  constexpr int TT = C::TT;       // stage rows
+  constexpr int TS4 = TT + 4;     // transposed tiles [DP][TS4]
+  constexpr int RS4 = DP + 4;     // row-major tiles [TT][RS4]
+  constexpr int NM = DP / 8;      // 16-byte operand loads per lane over the head dim
+  // The fp32 MFMA takes one operand element per lane and k-step, and the contraction order
+  // is free: over d, k-step kk = 4m + u of lane group g takes d = 8m + 4g + u, and over
+  // the stage rows, k-step j = 4jb + u takes row key_of_reg(j, g), 4 consecutive rows for
+  // consecutive u.  Either way one 16-byte LDS load gives a lane four k-steps.
+  __shared__ __attribute__((aligned(16))) float Qt[2][DP * TS4];
+  __shared__ __attribute__((aligned(16))) float Gt[2][DP * TS4];
+  __shared__ __attribute__((aligned(16))) float Qr[2][TT * RS4];
+  __shared__ __attribute__((aligned(16))) float Gr[2][TT * RS4];
+  __shared__ float lse_s[2][TT], dd_s[2][TT];
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
@@ -286,13 +341,15 @@ void bwd_dkdv_kernel(const BwdParams p) {
   const T* V = static_cast<const T*>(p.v) + bi * p.vs[0] + hi * p.vs[1];
   const T* dO = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1];
 
-  F kf[C::NKK], vf[C::NKK];
+  // this lane's key row of K and V at d = 8m + 4g .. + 3 (the B operands of S and dP)
+  f32x4 kf[NM], vf[NM];
   const int ksafe = key_ok ? my_key : 0;
 #pragma unroll
-  for (int kk = 0; kk < C::NKK; ++kk) {
-    const int d0 = kk * C::KSTEP + g * C::KP;
-    kf[kk] = load_frag<T>(K + (int64_t)ksafe * p.ks[2] + d0, key_ok && d0 < p.D);
-    vf[kk] = load_frag<T>(V + (int64_t)ksafe * p.vs[2] + d0, key_ok && d0 < p.D);
+  for (int m = 0; m < NM; ++m) {
+    const int d0 = 8 * m + 4 * g;
+    const bool ok = key_ok && d0 < p.D;
+    kf[m] = ok ? *reinterpret_cast<const f32x4*>(K + (int64_t)ksafe * p.ks[2] + d0) : f32x4{};
+    vf[m] = ok ? *reinterpret_cast<const f32x4*>(V + (int64_t)ksafe * p.vs[2] + d0) : f32x4{};
   }
   f32x16 dk[C::NDT], dv[C::NDT];
 #pragma unroll
@@ -300,23 +357,23 @@ void bwd_dkdv_kernel(const BwdParams p) {
     dk[dt] = f32x16{};
     dv[dt] = f32x16{};
   }
-  const int r_begin = p.causal ? (wg_key0 / C::TT) * C::TT : 0;
-  const int ntiles = (p.N - r_begin + C::TT - 1) / C::TT;
+  const int r_begin = p.causal ? (wg_key0 / TT) * TT : 0;
+  const int ntiles = (p.N - r_begin + TT - 1) / TT;
   Chunk16 qreg[F32Stage<DP, NT>::NCH], greg[F32Stage<DP, NT>::NCH];
   float lreg = 0.f, dreg = 0.f;
   auto gload = [&](int t0) {
     f32_stage_load<DP, NT>(qreg, Q, p.qs[2], t0, p.N, p.D, tid);
     f32_stage_load<DP, NT>(greg, dO, p.gs[2], t0, p.N, p.D, tid);
-    if (tid < C::TT) {
+    if (tid < TT) {
       const int ra = t0 + tid;
       lreg = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : kNegInf;
       dreg = ra < p.N ? p.d_row[(int64_t)bh * p.N + ra] : 0.f;
     }
   };
   auto sstore = [&](int buf) {
-    f32_stage_store<DP, NT>(qreg, Qt[buf], tid);
-    f32_stage_store<DP, NT>(greg, Gt[buf], tid);
-    if (tid < C::TT) {
+    f32_stage_store2<DP, NT, F32Stage<DP, NT>::NCH, TS4, RS4>(qreg, Qt[buf], Qr[buf], tid);
+    f32_stage_store2<DP, NT, F32Stage<DP, NT>::NCH, TS4, RS4>(greg, Gt[buf], Gr[buf], tid);
+    if (tid < TT) {
       lse_s[buf][tid] = lreg;
       dd_s[buf][tid] = dreg;
     }
@@ -328,16 +385,24 @@ void bwd_dkdv_kernel(const BwdParams p) {
   __syncthreads();
 
   for (int it = 0; it < ntiles; ++it) {
-    const int t0 = r_begin + it * C::TT, buf = it & 1;
+    const int t0 = r_begin + it * TT, buf = it & 1;
     const bool has_next = it + 1 < ntiles;
-    if (has_next) gload(t0 + C::TT);
-    const T* qt = Qt[buf];
-    const T* gt = Gt[buf];
+    if (has_next) gload(t0 + TT);
     f32x16 s = f32x16{}, dp = f32x16{};
+    {
+      // A operands: stage row swap23(c), d = 8m + 4g .. + 3
+      const float* qr = Qr[buf] + swap23(c) * RS4 + 4 * g;
+      const float* gr = Gr[buf] + swap23(c) * RS4 + 4 * g;
 #pragma unroll
-    for (int kk = 0; kk < C::NKK; ++kk) {
-      s = M::mma(a_frag<T, DP>(nullptr, qt, c, g, kk), kf[kk], s);
-      dp = M::mma(a_frag<T, DP>(nullptr, gt, c, g, kk), vf[kk], dp);
+      for (int m = 0; m < NM; ++m) {
+        const f32x4 qa = *reinterpret_cast<const f32x4*>(qr + 8 * m);
+        const f32x4 ga = *reinterpret_cast<const f32x4*>(gr + 8 * m);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          s = M::mma(qa[u], kf[m][u], s);
+          dp = M::mma(ga[u], vf[m][u], dp);
+        }
+      }
     }
     f32x16 pv;
 #pragma unroll
@@ -354,13 +419,18 @@ void bwd_dkdv_kernel(const BwdParams p) {
       s[r] = pr * (dp[r] - dd_s[buf][rl]);
     }
 #pragma unroll
-    for (int j = 0; j < C::NJ; ++j) {
-      const F bp = pv[j], bs = s[j];
+    for (int jb = 0; jb < 4; ++jb) {
+      const int row0 = 16 * (jb >> 1) + 8 * g + 4 * (jb & 1);  // key_of_reg(4 jb, g)
 #pragma unroll
       for (int dt = 0; dt < C::NDT; ++dt) {
-        const int off = (dt * 32 + c) * C::TS + key_of_reg(j * C::KP, g);
-        dv[dt] = M::mma(load_frag<T>(gt + off, true), bp, dv[dt]);
-        dk[dt] = M::mma(load_frag<T>(qt + off, true), bs, dk[dt]);
+        const int off = (dt * 32 + c) * TS4 + row0;
+        const f32x4 ga = *reinterpret_cast<const f32x4*>(Gt[buf] + off);
+        const f32x4 qa = *reinterpret_cast<const f32x4*>(Qt[buf] + off);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          dv[dt] = M::mma(ga[u], pv[4 * jb + u], dv[dt]);
+          dk[dt] = M::mma(qa[u], s[4 * jb + u], dk[dt]);
+        }
       }
     }
     if (has_next) sstore(buf ^ 1);
@@ -1001,10 +1071,7 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (stage < 0 || stage == 2) {
-      if (DP <= 64 && (int64_t)grid.x * grid.y >= 2 * 256)
-        hipLaunchKernelGGL((bwd_dkdv_kernel<T, DP, W, B, 2>), grid, dim3(64 * W), 0, st, p);
-      else
-        hipLaunchKernelGGL((bwd_dkdv_kernel<T, DP, W, B, 1>), grid, dim3(64 * W), 0, st, p);
+      hipLaunchKernelGGL((bwd_dkdv_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
       e = hipGetLastError();
     }
   }
