@@ -87,8 +87,8 @@ __device__ inline typename Mfma<T>::frag a_frag(const T* rm, const T* tr, int c,
 
 // fp32 stage staging, double-buffered: each thread first loads its 16-byte chunks of the
 // next TT rows into registers (f32_stage_load, issued before the current stage's MFMAs),
-// then writes them transposed ([DP][TS], TS = TT + 1) into the other LDS buffer
-// (f32_stage_store).  Rows >= row_end and d >= D read as zeros.
+// then writes them into the other LDS buffer (f32_stage_store2).  Rows >= row_end and
+// d >= D read as zeros.
 template <int DP, int NT>
 struct F32Stage {
   static constexpr int CPR = DP / 4;              // 16-byte chunks per row
@@ -112,23 +112,7 @@ __device__ inline void f32_stage_load(Chunk16 (&reg)[NR], const float* __restric
   });
 }
 
-template <int DP, int NT, int NR>
-__device__ inline void f32_stage_store(const Chunk16 (&reg)[NR], float* tr, int tid) {
-  using S = F32Stage<DP, NT>;
-  static_assert(NR == S::NCH, "one register chunk per staged chunk of this thread");
-  constexpr int TS = BwdCfg<float, DP>::TS;
-  static_for<0, S::NCH>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    const int ci = tid + i * NT;
-    if (S::TOTAL % NT == 0 || ci < S::TOTAL) {
-      const int r = ci / S::CPR, d0 = (ci % S::CPR) * 4;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) tr[(d0 + t) * TS + r] = __uint_as_float(reg[i][t]);
-    }
-  });
-}
-
-// fp32 dk/dv staging: the same register chunks written transposed with a 16-byte aligned
+// fp32 dk/dv staging: the register chunks written transposed with a 16-byte aligned
 // row stride TS4 (four consecutive stage rows of one d in one 16-byte load) and row-major
 // with stride RS4 (four consecutive d of one row in one 16-byte load).
 template <int DP, int NT, int NR, int TS4, int RS4>
