@@ -824,10 +824,13 @@ static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
 // Measured on MI355X (Phase 1 + Phase 2, 256- against 128-row workgroups): B8 H3 N197
 // 11 against 8 us, B1 H8 N1024 22 against 15 us, B8 H3 N1025 25 against 24 us, B1 H8 N4096
 // 64 against 70 us, B1 H8 N16384 617 against 703 us.
+// With a bias the 64-row waves hold the bias values of two row tiles and spill (252 bytes
+// per lane at D = 64), so biased sequences stay at 128 rows: B1 H8 d64 fp16 with an
+// [H, N, N] bias, forward 2K 0.068 -> 0.040 ms, 4K 0.211 -> 0.162 ms, 8K 0.688 -> 0.555 ms.
 constexpr int64_t kSmallSeq = 1024;
-int phase1_block_m(int dtype, int dp, int64_t n) {
+int phase1_block_m(int dtype, int dp, int64_t n, bool bias) {
   if (n <= 64) return 64;
-  if (dtype == ELSA_F32 || dp > 64) return 128;
+  if (dtype == ELSA_F32 || dp > 64 || bias) return 128;
   return n <= kSmallSeq ? 128 : 256;
 }
 
@@ -840,7 +843,8 @@ static hipError_t launch1h_wb(const Phase1Params& p, int block_m, hipStream_t st
     // 224 px forward 1.531 -> 1.469 ms, 512 px 4.371 -> 4.253 ms).
     if (block_m == 64) return b ? launch1h<T, DP, 1, 2, true>(p, st) : launch1h<T, DP, 2, 1, false>(p, st);
     if (block_m == 128) return b ? launch1h<T, DP, 1, 4, true>(p, st) : launch1h<T, DP, 1, 4, false>(p, st);
-    return b ? launch1h<T, DP, 2, 4, true>(p, st) : launch1h<T, DP, 2, 4, false>(p, st);
+    // the planner gives biased calls 128-row blocks (phase1_block_m); the grid follows the kernel
+    return b ? launch1h<T, DP, 1, 4, true>(p, st) : launch1h<T, DP, 2, 4, false>(p, st);
   } else {
     if (block_m == 64) return b ? launch1h<T, DP, 1, 2, true>(p, st) : launch1h<T, DP, 1, 2, false>(p, st);
     return b ? launch1h<T, DP, 1, 4, true>(p, st) : launch1h<T, DP, 1, 4, false>(p, st);

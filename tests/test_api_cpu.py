@@ -103,6 +103,18 @@ def test_plan_block_m_by_sequence_length(n, d, dtype, bm):
     assert rc == 0 and p.block_m == bm
 
 
+def test_plan_block_m_with_bias():
+    a = _args(n=16384)
+    bias = torch.zeros(1)  # only the pointer's presence matters to the planner
+    a.bias = _lib.bias_desc(bias, (0, 0, 16384, 1))
+    rc, p = _plan(a)
+    assert rc == 0 and p.block_m == 128
+    a = _args(n=49, d=32)
+    a.bias = _lib.bias_desc(bias, (0, 0, 49, 1))
+    rc, p = _plan(a)
+    assert rc == 0 and p.block_m == 64
+
+
 def test_plan_user_partition_and_chunk():
     rc, p = _plan(_args(n=513, bh=(1, 2), part=128, qc=128))
     assert rc == 0 and p.partition_len == 128 and p.partitions == 5 and p.q_chunk == 128
