@@ -86,13 +86,16 @@ int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
     int64_t p = cdiv(2048, q_tiles);
     p = std::min<int64_t>(p, std::max<int64_t>(1, n / 512));
     if (n >= 8192) p = std::max<int64_t>(p, 2);
-    // causal from 8K keys: 4096-key partitions.  About half of the causal workgroups
-    // have no keys to fold, and partitions of this width balance the rest best on
-    // MI355X (Phase 1 + Phase 2 at B1 H8 d64: 8K 0.147 ms against 0.156 at 1024-key
-    // partitions, 32K 1.354 ms against 1.514 at 16384).
-    if (a->is_causal && n >= 8192) p = std::max<int64_t>(2, n / 4096);
+    // causal from 8K keys: partitions of n/4 keys within [2048, 8192].  About half of the
+    // causal workgroups have no keys to fold; Phase 1 dispatches the rest longest first.
+    // Phase 1 + Phase 2 at B1 H8 d64 fp16 against 1024 / 2048 / 4096 / 8192-key partitions:
+    // 8K 0.114 / 0.114 / 0.119 / 0.187 ms, 16K 0.380 / 0.342 / 0.343 / 0.366 ms, 32K 1.518 /
+    // 1.344 / 1.227 / 1.199 ms.
+    if (a->is_causal && n >= 8192) p = cdiv(n, std::min<int64_t>(8192, std::max<int64_t>(2048, n / 4)));
     p = std::max<int64_t>(p, 1);
-    part = cdiv(cdiv(n, p), kt) * kt;
+    // causal partitions hold whole row blocks, which Phase 1's longest-first order needs
+    const int64_t unit = a->is_causal ? std::max<int64_t>(kt, bm) : kt;
+    part = cdiv(cdiv(n, p), unit) * unit;
     part = std::min<int64_t>(part, n);
   }
   const int64_t parts = cdiv(n, part);

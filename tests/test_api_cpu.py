@@ -82,10 +82,12 @@ def test_plan_partitions_cover_sequence(n, bh, d):
     assert p.q_chunk >= 1
 
 
-@pytest.mark.parametrize("n,parts", [(8192, 2), (16384, 4), (32768, 8), (65536, 16)])
-def test_plan_causal_uses_4096_key_partitions_from_8k(n, parts):
+@pytest.mark.parametrize("n,part,parts", [(8192, 2048, 4), (16384, 4096, 4), (32768, 8192, 4), (65536, 8192, 8),
+                                          (12000, 3072, 4)])
+def test_plan_causal_partitions_of_a_quarter_within_2k_8k_from_8k(n, part, parts):
     rc, p = _plan(_args(n=n, causal=1))
-    assert rc == 0 and p.partition_len == 4096 and p.partitions == parts
+    assert rc == 0 and p.partition_len == part and p.partitions == parts
+    assert p.partition_len % p.block_m == 0  # whole row blocks: Phase 1 dispatches longest first
 
 
 def test_plan_causal_short_sequences_keep_the_workgroup_target():
