@@ -83,7 +83,11 @@ int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
   } else {
     const int64_t q_rows = a->q_chunk > 0 ? std::min<int64_t>(a->q_chunk, n) : n;
     const int64_t q_tiles = bh * cdiv(q_rows, bm);
-    int64_t p = cdiv(2048, q_tiles);
+    // about 1024 Phase-1 workgroups (4 per CU): at B1 H8 d64 fp16 16K, Phase 1 + Phase 2 took
+    // 0.594 ms with 2 partitions against 0.605 ms with 4 (2048 workgroups); 64K 9.06 / 9.17 /
+    // 9.35 ms with 4 / 8 / 16; the forward at 1K and at ViT's 1025 and 4097 tokens (B8 H3)
+    // stays within 3% from 1 to 8 partitions
+    int64_t p = cdiv(1024, q_tiles);
     p = std::min<int64_t>(p, std::max<int64_t>(1, n / 512));
     if (n >= 8192) p = std::max<int64_t>(p, 2);
     // causal from 8K keys: partitions of n/4 keys within [2048, 8192].  About half of the
