@@ -97,9 +97,16 @@ int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
     // 1.344 / 1.227 / 1.199 ms.
     if (a->is_causal && n >= 8192) p = cdiv(n, std::min<int64_t>(8192, std::max<int64_t>(2048, n / 4)));
     p = std::max<int64_t>(p, 1);
-    // causal partitions hold whole row blocks, which Phase 1's longest-first order needs
-    const int64_t unit = a->is_causal ? std::max<int64_t>(kt, bm) : kt;
-    part = cdiv(cdiv(n, p), unit) * unit;
+    part = cdiv(cdiv(n, p), kt) * kt;
+    if (a->is_causal && p > 1) {  // one partition stays whole: its launch applies the finalize
+      // causal partitions hold whole row blocks, which Phase 1's longest-first order needs;
+      // the nearest multiple, not the next: a short causal launch has fewer workgroups than
+      // the chip holds and lasts as long as its longest one (B1 H8 d64 fp16, Phase 1 + Phase 2
+      // with 512 / 768-key partitions: 1025 tokens 0.024 / 0.029 ms, 2048 0.025 / 0.030 ms;
+      // 4097 tokens goes the other way, 0.049 / 0.044 ms)
+      const int64_t unit = std::max<int64_t>(kt, bm);
+      part = std::max<int64_t>(unit, (cdiv(n, p) + unit / 2) / unit * unit);
+    }
     part = std::min<int64_t>(part, n);
   }
   const int64_t parts = cdiv(n, part);

@@ -90,6 +90,17 @@ def test_plan_causal_partitions_of_a_quarter_within_2k_8k_from_8k(n, part, parts
     assert p.partition_len % p.block_m == 0  # whole row blocks: Phase 1 dispatches longest first
 
 
+def test_plan_causal_short_partitions_round_to_the_nearest_row_block():
+    rc, p = _plan(_args(n=1025, causal=1))
+    assert rc == 0 and p.block_m == 256 and p.partition_len == 512 and p.partitions == 3
+
+
+@pytest.mark.parametrize("n,d", [(300, 128), (197, 64), (49, 32)])
+def test_plan_causal_single_partition_stays_whole(n, d):
+    rc, p = _plan(_args(n=n, bh=(2, 2), d=d, causal=1))
+    assert rc == 0 and p.partitions == 1 and p.partition_len == n
+
+
 def test_plan_causal_short_sequences_keep_the_workgroup_target():
     rc_c, pc = _plan(_args(n=2048, causal=1))
     rc_n, pn = _plan(_args(n=2048))
