@@ -39,7 +39,10 @@ struct FwdCfg {
   static constexpr bool HALF = sizeof(T) == 2;
   static constexpr int KT = ((HALF && DP == 128) || (!HALF && DP >= 64)) ? 32 : 64;  // keys per LDS stage
   static constexpr int NSUB = KT / 32;
-  static constexpr int KPAD = HALF ? 8 : 1;
+  static constexpr int KPAD = HALF ? 8 : 4;  // fp32: K rows stay 16-byte aligned for 4-float loads
+  // fp32 V^T keeps stride KT + 1: its transposing scalar writes are conflict-free there, and
+  // 16-byte reads at stride KT + 4 cost more in those writes than they saved (16K Phase 1
+  // 4.68 against 4.52 ms)
   static constexpr int VPAD = HALF ? 8 : 1;
   static constexpr int KS = DP + KPAD;  // LDS row stride of K   [KT][KS]
   static constexpr int VS = KT + VPAD;  // LDS row stride of V^T [DP][VS]
@@ -165,9 +168,14 @@ __device__ inline void emit4(const Phase1Params& p, int64_t ridx, int64_t ooff, 
 
 template <typename T, int DP, int WAVES, bool HAS_BIAS>
 __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p) {
+  static_assert(sizeof(T) == 4, "fp32 fold (fp16 / bf16: phase1_half_kernel)");
   using C = FwdCfg<T, DP>;
   using M = Mfma<T>;
-  typedef typename M::frag F;
+  // The fp32 MFMA takes one operand element per lane and k-step, and the contraction order
+  // over d is free: k-step kk = 4m + u of lane group g takes d = 8m + 4g + u, so one 16-byte
+  // LDS load of a K row gives a lane four k-steps (4K Phase 1 0.328 -> 0.317 ms, 16K 4.573
+  // -> 4.515 ms against one 4-byte load per k-step).
+  constexpr int NM = DP / 8;
   constexpr int NT = 64 * WAVES;
   constexpr int BM = 32 * WAVES;
   constexpr int CPR = DP / C::CE;  // 16-byte chunks per key row
@@ -199,12 +207,12 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
   const T* __restrict__ K = static_cast<const T*>(p.k) + bi * p.ks[0] + hi * p.ks[1];
   const T* __restrict__ V = static_cast<const T*>(p.v) + bi * p.vs[0] + hi * p.vs[1];
 
-  // Q^T fragments (B operand of S^T = K Q^T): lane (c, g) holds Q[row c][d = kk*KSTEP + g*KP + t].
-  F qf[C::NKK];
+  // Q^T operand of S^T = K Q^T: lane (c, g) holds Q[row c][d = 8m + 4g .. + 3]
+  f32x4 qf[NM];
 #pragma unroll
-  for (int kk = 0; kk < C::NKK; ++kk) {
-    const int d0 = kk * C::KSTEP + g * C::KP;
-    qf[kk] = load_frag<T>(Q + (int64_t)(row_ok ? my_row : 0) * p.qs[2] + d0, row_ok && d0 < p.D);
+  for (int m = 0; m < NM; ++m) {
+    const int d0 = 8 * m + 4 * g;
+    qf[m] = (row_ok && d0 < p.D) ? *reinterpret_cast<const f32x4*>(Q + (int64_t)my_row * p.qs[2] + d0) : f32x4{};
   }
 
   Chunk16 kreg[NCH], vreg[NCH];
@@ -228,14 +236,7 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
     for (int i = 0; i < NCH; ++i) {
       const int ci = tid + i * NT;
       const int key = ci / CPR, d0 = (ci % CPR) * C::CE;
-      T* kd = &Ks[buf][key * C::KS + d0];
-      if constexpr (C::HALF) {
-        *reinterpret_cast<Chunk16*>(kd) = kreg[i];
-      } else {
-        const T* src = reinterpret_cast<const T*>(&kreg[i]);
-#pragma unroll
-        for (int e = 0; e < C::CE; ++e) kd[e] = src[e];
-      }
+      *reinterpret_cast<Chunk16*>(&Ks[buf][key * C::KS + d0]) = kreg[i];
       const T* vs = reinterpret_cast<const T*>(&vreg[i]);
 #pragma unroll
       for (int e = 0; e < C::CE; ++e) Vt[buf][(d0 + e) * C::VS + key] = vs[e];
@@ -266,9 +267,13 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
 #pragma unroll
     for (int sub = 0; sub < C::NSUB; ++sub) {
       s[sub] = f32x16{};
-      const T* krow = ks + (sub * 32 + swap23(c)) * C::KS + g * C::KP;
+      const T* krow = ks + (sub * 32 + swap23(c)) * C::KS + 4 * g;
 #pragma unroll
-      for (int kk = 0; kk < C::NKK; ++kk) s[sub] = M::mma(load_frag<T>(krow + kk * C::KSTEP, true), qf[kk], s[sub]);
+      for (int m = 0; m < NM; ++m) {
+        const f32x4 ka = *reinterpret_cast<const f32x4*>(krow + 8 * m);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) s[sub] = M::mma(ka[u], qf[m][u], s[sub]);
+      }
     }
 
     float mx = kNegInf;
@@ -323,22 +328,18 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
     }
     m_run = m_new;
 
-    // O^T += V^T P^T : A = V^T rows d, B = P^T straight from the S^T registers.
+    // O^T += V^T P^T : A = V^T rows d, B = P^T straight from the S^T registers; k-step
+    // 4 jb + u takes key key_of_reg(4 jb + u, g) = k0 + u.
 #pragma unroll
     for (int sub = 0; sub < C::NSUB; ++sub)
 #pragma unroll
-      for (int j = 0; j < C::NJ; ++j) {
-        F b;
-        if constexpr (C::KP == 1) {
-          b = s[sub][j];
-        } else {
-#pragma unroll
-          for (int t = 0; t < 8; ++t) b[t] = static_cast<T>(s[sub][j * 8 + t]);
-        }
+      for (int jb = 0; jb < 4; ++jb) {
+        const int k0 = sub * 32 + 16 * (jb >> 1) + 8 * g + 4 * (jb & 1);  // key_of_reg(4 jb, g)
 #pragma unroll
         for (int dt = 0; dt < C::NDT; ++dt) {
-          const T* vrow = vt + (dt * 32 + c) * C::VS + sub * 32 + key_of_reg(j * C::KP, g);
-          oacc[dt] = M::mma(load_frag<T>(vrow, true), b, oacc[dt]);
+          const T* vrow = vt + (dt * 32 + c) * C::VS + k0;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) oacc[dt] = M::mma(vrow[u], s[sub][4 * jb + u], oacc[dt]);
         }
       }
 
