@@ -112,10 +112,9 @@ __device__ inline void f32_stage_load(Chunk16 (&reg)[NR], const float* __restric
   });
 }
 
-// fp32 dk/dv staging: the register chunks written transposed with a 16-byte aligned
-// row stride TS4 (four consecutive stage rows of one d in one 16-byte load) and row-major
+// fp32 dk/dv staging: the register chunks written transposed (row stride TS) and row-major
 // with stride RS4 (four consecutive d of one row in one 16-byte load).
-template <int DP, int NT, int NR, int TS4, int RS4>
+template <int DP, int NT, int NR, int TS, int RS4>
 __device__ inline void f32_stage_store2(const Chunk16 (&reg)[NR], float* tr, float* rm, int tid) {
   using S = F32Stage<DP, NT>;
   static_assert(NR == S::NCH, "one register chunk per staged chunk of this thread");
@@ -125,7 +124,7 @@ __device__ inline void f32_stage_store2(const Chunk16 (&reg)[NR], float* tr, flo
     if (S::TOTAL % NT == 0 || ci < S::TOTAL) {
       const int r = ci / S::CPR, d0 = (ci % S::CPR) * 4;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) tr[(d0 + t) * TS4 + r] = __uint_as_float(reg[i][t]);
+      for (int t = 0; t < 4; ++t) tr[(d0 + t) * TS + r] = __uint_as_float(reg[i][t]);
       *reinterpret_cast<Chunk16*>(rm + r * RS4 + d0) = reg[i];
     }
   });
@@ -168,10 +167,9 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdParams p) {
 
 // ------------------------------------------------------------------ dq
 // fp32 only (the fp16 / bf16 kernel follows below).  The fp32 MFMA takes one operand
-// element per lane and k-step; the contraction orders are chosen so that one 16-byte LDS
-// load gives a lane four k-steps: over d, k-step kk = 4m + u of lane group g takes
-// d = 8m + 4g + u (row-major K and V tiles); over the stage keys, k-step j = 4jb + u takes
-// key key_of_reg(j, g), four consecutive keys for consecutive u (transposed K tile).
+// element per lane and k-step; over d the contraction order is k-step kk = 4m + u of lane
+// group g at d = 8m + 4g + u, so one 16-byte load of a row-major K or V row gives a lane
+// four k-steps.  The transposed K tile (dQ operand) keeps stride TT + 1 and 4-byte loads.
 template <typename T, int DP, int WAVES, bool HAS_BIAS>
 __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
   static_assert(sizeof(T) == 4, "fp32 kernel");
@@ -179,12 +177,12 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
   using M = Mfma<T>;
   constexpr int NT = 64 * WAVES, BM = 32 * WAVES;
   constexpr int TT = C::TT;       // keys per stage
-  constexpr int TS4 = TT + 4;     // transposed K tile [DP][TS4]
+  constexpr int TS1 = TT + 1;     // transposed K tile [DP][TS1]: conflict-free transposing writes
   constexpr int RS4 = DP + 4;     // row-major K and V tiles [TT][RS4]
   constexpr int NM = DP / 8;
   __shared__ __attribute__((aligned(16))) float Kr[TT * RS4];
   __shared__ __attribute__((aligned(16))) float Vr[TT * RS4];
-  __shared__ __attribute__((aligned(16))) float Kt[DP * TS4];
+  __shared__ __attribute__((aligned(16))) float Kt[DP * TS1];
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
@@ -233,7 +231,7 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
       *reinterpret_cast<f32x4*>(&Kr[r * RS4 + d0]) = kv;
       *reinterpret_cast<f32x4*>(&Vr[r * RS4 + d0]) = vv;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) Kt[(d0 + u) * TS4 + r] = kv[u];
+      for (int u = 0; u < 4; ++u) Kt[(d0 + u) * TS1 + r] = kv[u];
     }
     __syncthreads();
     f32x16 s = f32x16{}, dp = f32x16{};
@@ -268,7 +266,7 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
       const int k0 = 16 * (jb >> 1) + 8 * g + 4 * (jb & 1);  // key_of_reg(4 jb, g)
 #pragma unroll
       for (int dt = 0; dt < C::NDT; ++dt) {
-        const f32x4 ka = *reinterpret_cast<const f32x4*>(Kt + (dt * 32 + c) * TS4 + k0);
+        const float* ka = Kt + (dt * 32 + c) * TS1 + k0;
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc[dt] = M::mma(ka[u], s[4 * jb + u], acc[dt]);
       }
@@ -298,15 +296,16 @@ void bwd_dkdv_kernel(const BwdParams p) {
   using M = Mfma<T>;
   constexpr int NT = 64 * WAVES, BN = 32 * WAVES;
   constexpr int TT = C::TT;       // stage rows
-  constexpr int TS4 = TT + 4;     // transposed tiles [DP][TS4]
+  constexpr int TS1 = TT + 1;     // transposed tiles [DP][TS1]: conflict-free transposing writes
   constexpr int RS4 = DP + 4;     // row-major tiles [TT][RS4]
   constexpr int NM = DP / 8;      // 16-byte operand loads per lane over the head dim
   // The fp32 MFMA takes one operand element per lane and k-step, and the contraction order
-  // is free: over d, k-step kk = 4m + u of lane group g takes d = 8m + 4g + u, and over
-  // the stage rows, k-step j = 4jb + u takes row key_of_reg(j, g), 4 consecutive rows for
-  // consecutive u.  Either way one 16-byte LDS load gives a lane four k-steps.
-  __shared__ __attribute__((aligned(16))) float Qt[2][DP * TS4];
-  __shared__ __attribute__((aligned(16))) float Gt[2][DP * TS4];
+  // is free: over d, k-step kk = 4m + u of lane group g takes d = 8m + 4g + u, so one
+  // 16-byte load of a row-major Q or dO row gives a lane four k-steps.  The transposed tiles
+  // (dK / dV operands) keep stride TT + 1 and 4-byte loads: at a 16-byte aligned stride
+  // their transposing writes conflicted 4-way (16K 9.20 against 9.01 ms).
+  __shared__ __attribute__((aligned(16))) float Qt[2][DP * TS1];
+  __shared__ __attribute__((aligned(16))) float Gt[2][DP * TS1];
   __shared__ __attribute__((aligned(16))) float Qr[2][TT * RS4];
   __shared__ __attribute__((aligned(16))) float Gr[2][TT * RS4];
   __shared__ float lse_s[2][TT], dd_s[2][TT];
@@ -355,8 +354,8 @@ void bwd_dkdv_kernel(const BwdParams p) {
     }
   };
   auto sstore = [&](int buf) {
-    f32_stage_store2<DP, NT, F32Stage<DP, NT>::NCH, TS4, RS4>(qreg, Qt[buf], Qr[buf], tid);
-    f32_stage_store2<DP, NT, F32Stage<DP, NT>::NCH, TS4, RS4>(greg, Gt[buf], Gr[buf], tid);
+    f32_stage_store2<DP, NT, F32Stage<DP, NT>::NCH, TS1, RS4>(qreg, Qt[buf], Qr[buf], tid);
+    f32_stage_store2<DP, NT, F32Stage<DP, NT>::NCH, TS1, RS4>(greg, Gt[buf], Gr[buf], tid);
     if (tid < TT) {
       lse_s[buf][tid] = lreg;
       dd_s[buf][tid] = dreg;
@@ -407,13 +406,11 @@ void bwd_dkdv_kernel(const BwdParams p) {
       const int row0 = 16 * (jb >> 1) + 8 * g + 4 * (jb & 1);  // key_of_reg(4 jb, g)
 #pragma unroll
       for (int dt = 0; dt < C::NDT; ++dt) {
-        const int off = (dt * 32 + c) * TS4 + row0;
-        const f32x4 ga = *reinterpret_cast<const f32x4*>(Gt[buf] + off);
-        const f32x4 qa = *reinterpret_cast<const f32x4*>(Qt[buf] + off);
+        const int off = (dt * 32 + c) * TS1 + row0;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          dv[dt] = M::mma(ga[u], pv[4 * jb + u], dv[dt]);
-          dk[dt] = M::mma(qa[u], s[4 * jb + u], dk[dt]);
+          dv[dt] = M::mma(Gt[buf][off + u], pv[4 * jb + u], dv[dt]);
+          dk[dt] = M::mma(Qt[buf][off + u], s[4 * jb + u], dk[dt]);
         }
       }
     }
