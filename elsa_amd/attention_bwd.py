@@ -193,10 +193,12 @@ def twopass_attention_backward(
     return _backward(q, k, v, out, grad_out, bias_meta, is_causal=is_causal, row_m=row_m, row_z=row_z)
 
 
-def _backward(q, k, v, out, grad_out, bias_meta, *, is_causal, row_m, row_z, grads=None):
+def _backward(q, k, v, out, grad_out, bias_meta, *, is_causal, row_m, row_z, grads=None, dbias_out=None):
     """dq, dk, dv on the HIP library.  Operands are read in place when their layout allows
     (``_operand``); ``grads`` optionally names [B,H,N,D] (possibly strided) tensors to write
-    dq, dk, dv into, such as views of one fused qkv gradient."""
+    dq, dk, dv into, such as views of one fused qkv gradient.  With ``dbias_out`` (fp32
+    [bias_batch, bias_heads, N, N]) the same call also writes the bias gradient
+    (``elsa_bwd_dbias``: dS from the dk/dv kernel, summed over the broadcast dims)."""
     head_dim = int(q.shape[-1])
     scale = 1.0 / math.sqrt(head_dim)
     lib = _lib.load()
@@ -210,9 +212,18 @@ def _backward(q, k, v, out, grad_out, bias_meta, *, is_causal, row_m, row_z, gra
         dq, dk, dv = grads
     args = _bwd_args(q_c, k_c, v_c, out_c, do_c, row_m, row_z, dq, dk, dv, bias_meta, is_causal=is_causal,
                      scale=scale)
-    ws = _attach_workspace(lib, args, q.device)
-    with torch.cuda.device(q.device):
-        _lib.check(lib.elsa_bwd(ctypes.byref(args), _lib.stream_handle(q.device)), "elsa_bwd")
+    if dbias_out is None:
+        ws = _attach_workspace(lib, args, q.device)
+        with torch.cuda.device(q.device):
+            _lib.check(lib.elsa_bwd(ctypes.byref(args), _lib.stream_handle(q.device)), "elsa_bwd")
+    else:
+        bias_b, bias_h = int(dbias_out.shape[0]), int(dbias_out.shape[1])
+        nbytes = int(lib.elsa_bwd_dbias_workspace_bytes(ctypes.byref(args), bias_b, bias_h))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+        args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
+        with torch.cuda.device(q.device):
+            _lib.check(lib.elsa_bwd_dbias(ctypes.byref(args), dbias_out.data_ptr(), bias_b, bias_h,
+                                          _lib.stream_handle(q.device)), "elsa_bwd_dbias")
     del ws
     if padded:
         dq, dk, dv = (t[..., :head_dim] for t in (dq, dk, dv))
@@ -280,10 +291,15 @@ class _TwopassAttentionAutograd(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         q, k, v, out, bias, row_m, row_z = _saved(ctx)
+        if ctx.bias_requires_grad:  # dq, dk, dv and dbias in one call
+            meta, d32 = _dbias_target(q, bias)
+            dq, dk, dv = _backward(q, k, v, out, grad_out, meta, is_causal=ctx.is_causal, row_m=row_m, row_z=row_z,
+                                   dbias_out=d32)
+            return dq, dk, dv, d32.reshape(bias.shape).to(bias.dtype), None, None, None, None
         dq, dk, dv = twopass_attention_backward(
             q, k, v, out, grad_out, bias=bias, is_causal=ctx.is_causal, row_m=row_m, row_z=row_z, **ctx.bwd_kwargs
         )
-        return dq, dk, dv, _dbias(ctx, q, k, v, out, grad_out, bias, row_m, row_z), None, None, None, None
+        return dq, dk, dv, None, None, None, None, None
 
 
 class _TwopassQkvAutograd(torch.autograd.Function):
@@ -307,9 +323,14 @@ class _TwopassQkvAutograd(torch.autograd.Function):
         batch, heads, seq_len, _ = map(int, q.shape)
         dqkv = torch.empty_like(qkv, memory_format=torch.contiguous_format)
         grads = dqkv.permute(2, 0, 3, 1, 4).unbind(0)
+        if ctx.bias_requires_grad:  # dq, dk, dv and dbias in one call
+            meta, d32 = _dbias_target(q, bias)
+            _backward(q, k, v, out, grad_out, meta, is_causal=ctx.is_causal, row_m=row_m, row_z=row_z, grads=grads,
+                      dbias_out=d32)
+            return dqkv, d32.reshape(bias.shape).to(bias.dtype), None, None, None
         meta = _canonical_bias(bias, batch=batch, heads=heads, seq_len=seq_len, device=q.device)
         _backward(q, k, v, out, grad_out, meta, is_causal=ctx.is_causal, row_m=row_m, row_z=row_z, grads=grads)
-        return dqkv, _dbias(ctx, q, k, v, out, grad_out, bias, row_m, row_z), None, None, None
+        return dqkv, None, None, None, None
 
 
 def _save(ctx, inputs, out, bias, row_m, row_z, is_causal, bwd_kwargs):
@@ -326,10 +347,13 @@ def _saved(ctx):
     return (*inputs, out, saved_bias if ctx.has_bias else None, row_m, row_z)
 
 
-def _dbias(ctx, q, k, v, out, grad_out, bias, row_m, row_z):
-    if not ctx.bias_requires_grad:
-        return None
-    return _dense_bias_backward(q, k, v, out, grad_out, bias=bias, is_causal=ctx.is_causal, row_m=row_m, row_z=row_z)
+def _dbias_target(q, bias):
+    """The bias's canonical view and an fp32 gradient of its [1|B, 1|H, N, N] shape."""
+    batch, heads, seq_len, _ = map(int, q.shape)
+    meta = _canonical_bias(bias, batch=batch, heads=heads, seq_len=seq_len, device=q.device)
+    bias_b = 1 if meta.stride_b == 0 else batch
+    bias_h = 1 if meta.stride_h == 0 else heads
+    return meta, torch.empty((bias_b, bias_h, seq_len, seq_len), dtype=torch.float32, device=q.device)
 
 
 def _split_train_kwargs(bwd_block_m, bwd_block_n, bwd_num_warps, bwd_num_stages, bwd_input_precision, fwd_kwargs):

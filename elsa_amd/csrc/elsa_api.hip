@@ -472,6 +472,62 @@ int elsa_dbias(const elsa_bwd_args* a, float* dbias, int32_t bias_batch, int32_t
   return ELSA_OK;
 }
 
+// The fused dbias needs dS = p * (dP - D) for every (b, h, row, key) in fp32: straight into
+// dbias when the bias broadcasts over nothing, else into the workspace and then summed.  Up
+// to this many bytes of dS; beyond, dbias is recomputed by elsa_dbias's own kernel.
+static constexpr size_t kFusedDbiasBytes = size_t(1) << 30;
+
+static size_t ds_bytes(const elsa_bwd_args* a) {
+  return (size_t)a->batch * a->heads * a->seq_len * a->seq_len * sizeof(float);
+}
+
+size_t elsa_bwd_dbias_workspace_bytes(const elsa_bwd_args* a, int32_t bias_batch, int32_t bias_heads) {
+  if (!a || a->batch <= 0 || a->heads <= 0 || a->seq_len <= 0 || bias_batch <= 0 || bias_heads <= 0) return 0;
+  if (ds_bytes(a) > kFusedDbiasBytes) {
+    return std::max(elsa_bwd_workspace_bytes(a), elsa_dbias_workspace_bytes(a, bias_batch, bias_heads));
+  }
+  const bool direct = bias_batch == a->batch && bias_heads == a->heads;
+  if (direct) return elsa_bwd_workspace_bytes(a);
+  const int ns = elsa::dbias_sum_splits(a->batch, a->heads, bias_batch, bias_heads);
+  const size_t part = ns > 1 ? align256((size_t)ns * bias_batch * bias_heads * a->seq_len * a->seq_len * 4) : 0;
+  return elsa_bwd_workspace_bytes(a) + align256(ds_bytes(a)) + part;
+}
+
+int elsa_bwd_dbias(const elsa_bwd_args* a, float* dbias, int32_t bias_batch, int32_t bias_heads, void* stream) {
+  int rc = check_bwd(a, kUseGrads);
+  if (rc) return rc;
+  if (!dbias || !a->bias.ptr) return fail(ELSA_ERR_INVALID, "dbias and a bias are required");
+  if (!(bias_batch == 1 || bias_batch == a->batch) || !(bias_heads == 1 || bias_heads == a->heads))
+    return fail(ELSA_ERR_INVALID, "dbias shape [%d,%d] does not broadcast against [%d,%d]", bias_batch, bias_heads,
+                a->batch, a->heads);
+  const size_t need = elsa_bwd_dbias_workspace_bytes(a, bias_batch, bias_heads);
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(ELSA_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", a->workspace_bytes,
+                need);
+  if (ds_bytes(a) > kFusedDbiasBytes) {  // the backward, then dbias with its own recompute
+    if ((rc = elsa_bwd_stage(a, -1, stream))) return rc;
+    return elsa_dbias(a, dbias, bias_batch, bias_heads, stream);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool direct = bias_batch == a->batch && bias_heads == a->heads;
+  float* ds = direct ? dbias
+                     : reinterpret_cast<float*>(static_cast<char*>(a->workspace) + elsa_bwd_workspace_bytes(a));
+  hipError_t e = hipSuccess;
+  // causal dk/dv workgroups skip the stages above their keys: those dS entries stay zero
+  if (a->is_causal && (e = elsa::launch_zero_fill(ds, (int64_t)(ds_bytes(a) / sizeof(float)), st)) != hipSuccess)
+    return hip_fail(e, "zero fill");
+  elsa::BwdParams p = bwd_params(a);
+  p.ds_out = ds;
+  if ((e = elsa::launch_bwd(p, a->dtype, -1, st)) != hipSuccess) return hip_fail(e, "backward launch");
+  if (!direct) {
+    float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(ds) + align256(ds_bytes(a)));
+    if ((e = elsa::launch_dbias_sum(ds, dbias, a->batch, a->heads, a->seq_len, bias_batch, bias_heads, part, st)) !=
+        hipSuccess)
+      return hip_fail(e, "dbias sum launch");
+  }
+  return ELSA_OK;
+}
+
 int elsa_debug_mfma(int32_t variant, const void* a, const void* b, float* d, void* stream) {
   if (variant < 0 || variant > 2) return fail(ELSA_ERR_INVALID, "variant must be 0, 1 or 2");
   if (!a || !b || !d) return fail(ELSA_ERR_INVALID, "null pointer");

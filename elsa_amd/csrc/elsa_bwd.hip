@@ -400,6 +400,9 @@ void bwd_dkdv_kernel(const BwdParams p) {
       const float pr = ok ? fast_exp2(x - lse) : 0.f;
       pv[r] = pr;
       s[r] = pr * (dp[r] - dd_s[buf][rl]);
+      if constexpr (HAS_BIAS) {
+        if (p.ds_out != nullptr && key_ok && row < p.N) p.ds_out[((int64_t)bh * p.N + row) * p.N + my_key] = s[r];
+      }
     }
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
@@ -826,6 +829,14 @@ static_for<0, NCH>([&](auto I) {
                 const float x = fmaf(s[8 * j + t], p.scale_log2, -lr);
                 pr[t] = ok ? fast_exp2(fmaf(load_bias_b(p.bias, bi, hi, row, my_key), kLog2e, x)) : 0.f;
               }
+              if (p.ds_out != nullptr && key_ok[kt]) {  // lanes of one t: 32 consecutive keys of a row
+                float* dso = p.ds_out + (int64_t)bh * p.N * p.N + my_key;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                  const int row = t0 + sub * 32 + key_of_reg(8 * j + t, g);
+                  if (row < p.N) dso[(int64_t)row * p.N] = pr[t] * dp[8 * j + t];
+                }
+              }
             } else {
 #pragma unroll
               for (int t = 0; t < 8; ++t) pr[t] = fast_exp2(fmaf(s[8 * j + t], p.scale_log2, t < 4 ? -l0[t] : -l1[t - 4]));
@@ -1014,6 +1025,65 @@ __global__ __launch_bounds__(256) void dbias_reduce_kernel(const float* part, fl
   float acc = 0.f;
   for (int sp = 0; sp < nsplit; ++sp) acc += part[sp * n + i];
   dbias[i] = acc;
+}
+
+// dbias[bb', hb', i, j] = sum over the (b, h) pairs broadcast onto (bb', hb') of ds[b, h, i, j].
+// The pairs (b-major, increasing) are cut into nsplit contiguous ranges; each range's sum goes
+// to part[split] (to dbias when nsplit == 1) and dbias_reduce_kernel adds the ranges in order,
+// so the result does not depend on scheduling.  grid: x = blocks of 256 elements of one
+// (bb', hb') plane, y = bias head, z = bias batch x nsplit.
+__global__ __launch_bounds__(256) void dbias_sum_kernel(const float* __restrict__ ds, float* __restrict__ dbias,
+                                                        int B, int H, int N, int bias_batch, int bias_heads, int nsplit,
+                                                        float* __restrict__ part) {
+  const int64_t nn = (int64_t)N * N;
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= nn) return;
+  const int hb = blockIdx.y, bb = blockIdx.z / nsplit, split = blockIdx.z - bb * nsplit;
+  const int b_lo = bias_batch == 1 ? 0 : bb, nb = bias_batch == 1 ? B : 1;
+  const int h_lo = bias_heads == 1 ? 0 : hb, nh = bias_heads == 1 ? H : 1;
+  const int64_t pairs = (int64_t)nb * nh;
+  const int64_t r_lo = pairs * split / nsplit, r_hi = pairs * (split + 1) / nsplit;
+  float acc = 0.f;
+  for (int64_t r = r_lo; r < r_hi; ++r) {
+    const int b = b_lo + (int)(r / nh), h = h_lo + (int)(r % nh);
+    acc += ds[((int64_t)b * H + h) * nn + e];
+  }
+  const int64_t plane = (int64_t)bias_batch * bias_heads * nn;
+  (nsplit == 1 ? dbias : part + split * plane)[((int64_t)bb * bias_heads + hb) * nn + e] = acc;
+}
+
+__global__ __launch_bounds__(256) void zero_fill_kernel(float* dst, int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i + 3 < n) {
+    *reinterpret_cast<f32x4*>(dst + i) = f32x4{};
+  } else {
+    for (int64_t k = i; k < n; ++k) dst[k] = 0.f;
+  }
+}
+
+int dbias_sum_splits(int B, int H, int bias_batch, int bias_heads) {
+  const int64_t pairs = (int64_t)(bias_batch == 1 ? B : 1) * (bias_heads == 1 ? H : 1);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(256, (pairs + 63) / 64));  // ranges of about 64 pairs
+}
+
+hipError_t launch_dbias_sum(const float* ds, float* dbias, int B, int H, int N, int bias_batch, int bias_heads,
+                            float* part, hipStream_t st) {
+  const int64_t nn = (int64_t)N * N;
+  const int nsplit = part ? dbias_sum_splits(B, H, bias_batch, bias_heads) : 1;
+  hipLaunchKernelGGL(dbias_sum_kernel,
+                     dim3((unsigned)((nn + 255) / 256), (unsigned)bias_heads, (unsigned)(bias_batch * nsplit)),
+                     dim3(256), 0, st, ds, dbias, B, H, N, bias_batch, bias_heads, nsplit, part);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || nsplit == 1) return e;
+  const int64_t n = (int64_t)bias_batch * bias_heads * nn;
+  hipLaunchKernelGGL(dbias_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, dbias, nsplit, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_fill(float* dst, int64_t n, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, st, dst, n);
+  return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ launchers

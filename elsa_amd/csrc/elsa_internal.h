@@ -89,6 +89,8 @@ struct BwdParams {
   BiasView bias;
   float* d_row;    // [BH, N]
   float* lse_row;  // [BH, N]
+  // biased dk/dv kernels: when set, also store dS = p * (dP - D) in fp32, [BH, N, N]
+  float* ds_out;
   int H, N, D, BH;
   int causal;
   float scale;       // 1/sqrt(D_model)
@@ -106,5 +108,13 @@ int dbias_splits(int N, int batch, int heads, int bias_batch, int bias_heads);
 hipError_t launch_dbias(const BwdParams& p, float* dbias, int bias_batch, int bias_heads, int dtype, int nsplit,
                         float* part, hipStream_t stream);
 hipError_t launch_debug_mfma(int variant, const void* a, const void* b, float* d, hipStream_t stream);
+// dbias[bb', hb'] = sum over the (b, h) pairs broadcast onto it of ds[b, h], in a fixed order;
+// with part (dbias_sum_splits * bias_batch * bias_heads * N * N floats) the pairs are summed in
+// ranges across workgroups and the ranges added in order.
+int dbias_sum_splits(int B, int H, int bias_batch, int bias_heads);
+hipError_t launch_dbias_sum(const float* ds, float* dbias, int B, int H, int N, int bias_batch, int bias_heads,
+                            float* part, hipStream_t stream);
+// n floats of zeros (a kernel, so that graph capture records no memset node)
+hipError_t launch_zero_fill(float* dst, int64_t n, hipStream_t stream);
 
 }  // namespace elsa

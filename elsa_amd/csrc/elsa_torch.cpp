@@ -151,19 +151,22 @@ at::Tensor bwd_call(const at::Tensor& q, const at::Tensor& k, const at::Tensor& 
   b.dq_layout = layout_of(dq);
   b.dk_layout = layout_of(dk);
   b.dv_layout = layout_of(dv);
-  const size_t ws_bytes = elsa_bwd_workspace_bytes(&b);
-  const at::Tensor ws = bytes(q, ws_bytes);
-  b.workspace = ws.data_ptr();
-  b.workspace_bytes = ws_bytes;
-  check(elsa_bwd(&b, current_stream()), "elsa_bwd");
-  if (!bias.defined() || !dbias_wanted) return at::Tensor();
+  if (!bias.defined() || !dbias_wanted) {
+    const size_t ws_bytes = elsa_bwd_workspace_bytes(&b);
+    const at::Tensor ws = bytes(q, ws_bytes);
+    b.workspace = ws.data_ptr();
+    b.workspace_bytes = ws_bytes;
+    check(elsa_bwd(&b, current_stream()), "elsa_bwd");
+    return at::Tensor();
+  }
+  // dq, dk, dv and dbias in one call (dS from the dk/dv kernel)
   const int32_t bb = static_cast<int32_t>(bias.size(0)), bhd = static_cast<int32_t>(bias.size(1));
   at::Tensor d32 = at::empty({bb, bhd, N, N}, q.options().dtype(at::kFloat));
-  const size_t need = elsa_dbias_workspace_bytes(&b, bb, bhd);
-  const at::Tensor ws2 = bytes(q, need);
-  b.workspace = ws2.data_ptr();
+  const size_t need = elsa_bwd_dbias_workspace_bytes(&b, bb, bhd);
+  const at::Tensor ws = bytes(q, need);
+  b.workspace = ws.data_ptr();
   b.workspace_bytes = need;
-  check(elsa_dbias(&b, d32.data_ptr<float>(), bb, bhd, current_stream()), "elsa_dbias");
+  check(elsa_bwd_dbias(&b, d32.data_ptr<float>(), bb, bhd, current_stream()), "elsa_bwd_dbias");
   return d32.to(bias.scalar_type());
 }
 

@@ -171,6 +171,17 @@ size_t elsa_dbias_workspace_bytes(const elsa_bwd_args* args, int32_t bias_batch,
 int elsa_dbias(const elsa_bwd_args* args, float* dbias, int32_t bias_batch, int32_t bias_heads,
                void* stream);
 
+/* dq, dk, dv and dbias in one call: the dk/dv kernel stores dS = p*(dP - D) (fp32), which is
+ * dbias itself when the bias broadcasts over nothing and is otherwise summed over the
+ * broadcast (b, h) pairs in a fixed order.  Replaces elsa_bwd followed by elsa_dbias (the
+ * reference's backward launches and its _dbias_dense_kernel, attention_bwd.py:765-838 and
+ * :926-971), whose dbias kernel recomputes S and dP.  The dS buffer is limited to 1 GiB
+ * (B*H*N*N floats); past that the call runs elsa_bwd and elsa_dbias.  No counterpart in the
+ * reference as a single call. */
+size_t elsa_bwd_dbias_workspace_bytes(const elsa_bwd_args* args, int32_t bias_batch, int32_t bias_heads);
+int elsa_bwd_dbias(const elsa_bwd_args* args, float* dbias, int32_t bias_batch, int32_t bias_heads,
+                   void* stream);
+
 /* Device check of the MFMA operand/result layout: variant 0 fp16, 1 bf16, 2 fp32.
  * a, b: [64 lanes][KP] operand elements; d: [64 lanes][16] floats. */
 int elsa_debug_mfma(int32_t variant, const void* a, const void* b, float* d, void* stream);

@@ -168,6 +168,25 @@ def test_bwd_and_dbias_reject_bad_args_without_launching():
     assert lib.elsa_debug_mfma(5, 1, 1, 1, None) == _lib.ELSA_ERR_INVALID
 
 
+def test_bwd_dbias_rejects_bad_args_and_sizes_its_workspace():
+    lib = _lib.load()
+    b = _lib.BwdArgs()
+    b.batch, b.heads, b.seq_len, b.head_dim, b.dtype = 2, 3, 64, 64, _lib.ELSA_F16
+    b.q = b.k = b.v = b.out = b.dout = b.dq = b.dk = b.dv = b.row_m = b.row_z = 256
+    rows = lib.elsa_bwd_workspace_bytes(ctypes.byref(b))
+    ds = 2 * 3 * 64 * 64 * 4
+    # dbias of the bias's own shape is dS itself; a broadcast bias needs the dS buffer
+    assert lib.elsa_bwd_dbias_workspace_bytes(ctypes.byref(b), 2, 3) == rows
+    assert lib.elsa_bwd_dbias_workspace_bytes(ctypes.byref(b), 1, 3) == rows + ds
+    assert lib.elsa_bwd_dbias(ctypes.byref(b), 256, 2, 3, None) == _lib.ELSA_ERR_INVALID  # no bias
+    assert "bias" in lib.elsa_last_error().decode()
+    bias = torch.zeros(1)
+    b.bias = _lib.bias_desc(bias, (0, 64 * 64, 64, 1))
+    assert lib.elsa_bwd_dbias(ctypes.byref(b), 256, 3, 3, None) == _lib.ELSA_ERR_INVALID  # 3 does not broadcast to 2
+    assert lib.elsa_bwd_dbias(ctypes.byref(b), 256, 1, 3, None) == _lib.ELSA_ERR_WORKSPACE
+    assert lib.elsa_bwd_dbias(ctypes.byref(b), None, 1, 3, None) == _lib.ELSA_ERR_INVALID
+
+
 def test_bwd_layout_rules_without_launching():
     lib = _lib.load()
     b = _lib.BwdArgs()

@@ -328,3 +328,60 @@ def test_cpp_and_python_training_paths_agree(dt, causal, bias):
     for a, ref in zip(res[0], res[1]):
         if ref is not None:
             assert torch.equal(a, ref)
+
+
+@pytest.mark.parametrize("dt,shape,bias_shape,causal", [
+    ("fp16", (2, 3, 197, 64), (2, 3, 197, 197), False),   # dbias is dS itself
+    ("bf16", (2, 3, 130, 64), (1, 3, 130, 130), True),    # summed over the batch, causal zeros
+    ("fp32", (4, 2, 49, 32), (49, 49), False),            # summed over batch and heads
+    ("fp16", (8, 3, 49, 32), (8, 1, 49, 49), True),       # summed over heads
+    ("fp32", (1, 2, 300, 128), (1, 2, 300, 300), True),   # D = 128
+])
+def test_bwd_dbias_matches_bwd_then_dbias(dt, shape, bias_shape, causal):
+    """elsa_bwd_dbias (dS stored by the dk/dv kernel, summed over the broadcast dims) against
+    elsa_bwd followed by elsa_dbias (which recomputes S and dP): the same dq, dk, dv bits and
+    the same dbias up to the fp32 summation order."""
+    import ctypes
+
+    from elsa_amd import _lib
+    from elsa_amd.attention import _canonical_bias
+    from elsa_amd.attention_bwd import _bwd_args
+
+    describe(f"elsa_bwd_dbias {dt} {shape} bias {bias_shape} causal={causal}")
+    b, h, n, d = shape
+    q, k, v, do = O.make_inputs(shape, seed=n + d, dtype=dt, with_dout=True, dout_scale=0.3)
+    bias = (np.random.default_rng(n).standard_normal(bias_shape) * 0.5).astype(np.float32)
+    qd, kd, vd, dod = (dev(x, dt) for x in (q, k, v, do))
+    bd = dev(bias, dt)
+    out, rm, rz = elsa_amd.twopass_attention_with_state(qd, kd, vd, bias=bd, is_causal=causal)
+    lib = _lib.load()
+    meta = _canonical_bias(bd, batch=b, heads=h, seq_len=n, device=qd.device)
+    bias_b = 1 if meta.stride_b == 0 else b
+    bias_h = 1 if meta.stride_h == 0 else h
+    sh = _lib.stream_handle(qd.device)
+
+    def call(fused):
+        grads = tuple(torch.full_like(qd, float("nan")) for _ in range(3))
+        db = torch.full((bias_b, bias_h, n, n), float("nan"), dtype=torch.float32, device=qd.device)
+        args = _bwd_args(qd, kd, vd, out, dod, rm, rz, *grads, meta, is_causal=causal, scale=1 / np.sqrt(d))
+        if fused:
+            nbytes = int(lib.elsa_bwd_dbias_workspace_bytes(ctypes.byref(args), bias_b, bias_h))
+        else:
+            nbytes = int(lib.elsa_dbias_workspace_bytes(ctypes.byref(args), bias_b, bias_h))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=qd.device)
+        args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
+        if fused:
+            _lib.check(lib.elsa_bwd_dbias(ctypes.byref(args), db.data_ptr(), bias_b, bias_h, sh), "elsa_bwd_dbias")
+        else:
+            _lib.check(lib.elsa_bwd(ctypes.byref(args), sh), "elsa_bwd")
+            _lib.check(lib.elsa_dbias(ctypes.byref(args), db.data_ptr(), bias_b, bias_h, sh), "elsa_dbias")
+        torch.cuda.synchronize()
+        return grads, db
+
+    (g1, db1), (g2, db2) = call(True), call(False)
+    for name, a, ref in zip("qkv", g1, g2):
+        assert torch.equal(a, ref), f"d{name} differs"
+    x, y = host(db1), host(db2)
+    assert np.isfinite(x).all()
+    pairs = (b * h) // (bias_b * bias_h)
+    assert np.abs(x - y).max() <= 1e-6 * max(1.0, np.abs(y).max()) * pairs ** 0.5 + 1e-7
