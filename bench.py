@@ -121,6 +121,43 @@ def _flops_fwd(b, h, n, d, causal):
     return 4.0 * b * h * d * (n * (n + 1) / 2 if causal else n * n)
 
 
+def _mfma_ceiling(args, lib, dev, stream) -> float:
+    """TFLOP/s of elsa_debug_mfma_rate on operands drawn as the inputs are (``--fill``)."""
+    import torch
+
+    from elsa_amd import _lib
+
+    variant, kp, flop, iters = {"fp16": (0, 8, 32768, 20000), "bf16": (1, 8, 32768, 20000),
+                                "fp32": (2, 1, 4096, 2000)}[args.dtype]
+    dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[args.dtype]
+    x = torch.randn(16 * 256 * kp, generator=torch.Generator().manual_seed(7))
+    if args.fill == "sign":
+        x = x.sign()
+    elif args.fill != "randn":
+        x = torch.full_like(x, 0.0 if args.fill == "zeros" else 0.5)
+    src = x.to(dt).to(dev)
+    wgs = 2048
+    out = torch.empty(wgs * 256, dtype=torch.float32, device=dev)
+    sh = stream.cuda_stream
+
+    def launch():
+        _lib.check(lib.elsa_debug_mfma_rate(variant, src.data_ptr(), out.data_ptr(), iters, wgs, sh),
+                   "elsa_debug_mfma_rate")
+
+    launch()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(3):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 3
+    tflops = wgs * 4 * iters * 8 * flop / (ms * 1e-3) / 1e12
+    print(f"bench: MFMA ceiling ({args.fill} operands) {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    return tflops
+
+
 def main() -> int:
     args = _args()
     if args.summarize_pmc:
@@ -220,6 +257,9 @@ def main() -> int:
     print("bench: kernels " + ", ".join(f"{k_}={v_:.3f}ms" for k_, v_ in kern_ms.items()), file=sys.stderr,
           flush=True)
 
+    # ---- the matrix cores' sustained rate on operands with this run's value statistics
+    ceiling = _mfma_ceiling(args, lib, dev, stream)
+
     # ---- latency ratio against PyTorch's SDPA on the same inputs, the reference's headline
     # comparison (README.md:55-58: ELSA / FlashAttention on A100), for fp16 only
     vs_sdpa = _vs_sdpa(args, q, k, v, do, causal) if args.dtype == "fp16" else None
@@ -312,6 +352,15 @@ def main() -> int:
         "max_abs_sampled_fwd": max_abs,
         "kernels": kernels,
         "roofline": roofline,
+    }
+    # executed MFMA work per launch (the dq kernel recomputes S and dP: 3 GEMMs of N^2 d)
+    executed = {"phase1_fold": f_fwd, "bwd_dq": 1.5 * f_fwd, "bwd_dkdv": 2.0 * f_fwd}
+    result["mfma_ceiling"] = {
+        "fill": args.fill, "tflops": round(ceiling, 1), "frac_peak": round(ceiling / peak, 4),
+        "what": "sustained v_mfma_f32_32x32x* rate of 8 independent chains per wave on operands drawn like the "
+                "inputs (elsa_debug_mfma_rate); the power limit sets it below the nominal peak",
+        "executed_frac_of_ceiling": {n: round(w / (kern_ms[n] * 1e-3) / 1e12 / ceiling, 4)
+                                     for n, w in executed.items()},
     }
     if vs_sdpa is not None:
         result["vs_sdpa"] = vs_sdpa

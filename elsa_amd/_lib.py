@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "elsa_bwd_dbias",
     "elsa_bwd_dbias_workspace_bytes",
     "elsa_debug_mfma",
+    "elsa_debug_mfma_rate",
 )
 
 
@@ -176,8 +177,9 @@ def load() -> ctypes.CDLL:
     lib.elsa_bwd_dbias_workspace_bytes.argtypes = [ctypes.POINTER(BwdArgs), c_int32, c_int32]
     lib.elsa_bwd_dbias.argtypes = [ctypes.POINTER(BwdArgs), c_void_p, c_int32, c_int32, c_void_p]
     lib.elsa_debug_mfma.argtypes = [c_int32, c_void_p, c_void_p, c_void_p, c_void_p]
+    lib.elsa_debug_mfma_rate.argtypes = [c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p]
     for fn in ("elsa_fwd_plan_get", "elsa_fwd", "elsa_phase1", "elsa_phase2", "elsa_bwd", "elsa_bwd_stage", "elsa_row_stats",
-               "elsa_dbias", "elsa_bwd_dbias", "elsa_debug_mfma"):
+               "elsa_dbias", "elsa_bwd_dbias", "elsa_debug_mfma", "elsa_debug_mfma_rate"):
         getattr(lib, fn).restype = c_int32
     if lib.elsa_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{LIB_PATH}: ABI version {lib.elsa_abi_version()} != {ABI_VERSION}")

@@ -536,4 +536,15 @@ int elsa_debug_mfma(int32_t variant, const void* a, const void* b, float* d, voi
   return ELSA_OK;
 }
 
+int elsa_debug_mfma_rate(int32_t variant, const void* src, float* out, int32_t iters, int32_t workgroups,
+                         void* stream) {
+  if (variant < 0 || variant > 2) return fail(ELSA_ERR_INVALID, "variant must be 0, 1 or 2");
+  if (!src || !out) return fail(ELSA_ERR_INVALID, "null pointer");
+  if (iters < 1 || iters > 1000000) return fail(ELSA_ERR_INVALID, "iters must be in [1, 1000000]");
+  if (workgroups < 1 || workgroups > 65536) return fail(ELSA_ERR_INVALID, "workgroups must be in [1, 65536]");
+  hipError_t e = elsa::launch_debug_mfma_rate(variant, src, out, iters, workgroups, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "debug_mfma_rate launch");
+  return ELSA_OK;
+}
+
 }  // extern "C"

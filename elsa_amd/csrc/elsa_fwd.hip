@@ -928,4 +928,56 @@ hipError_t launch_debug_mfma(int variant, const void* a, const void* b, float* d
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------ MFMA rate probe
+// Sustained matrix-core rate on given operand values: every lane of a 256-thread work-group
+// holds 8 A and 8 B fragments (src: [16][256][KP] elements, fragment 2j is A and 2j+1 is B
+// of chain j) and advances 8 independent 32x32 accumulator chains `iters` times.  The
+// accumulator sums are written out so that nothing is dead code.
+template <typename T>
+__global__ __launch_bounds__(256) void debug_mfma_rate_kernel(const T* __restrict__ src, float* out, int iters) {
+  using M = Mfma<T>;
+  typedef typename M::frag F;
+  constexpr int NJ = 8, KP = M::KP;
+  const int lane = threadIdx.x;
+  F a[NJ], b[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if constexpr (KP == 1) {
+      a[j] = src[(2 * j) * 256 + lane];
+      b[j] = src[(2 * j + 1) * 256 + lane];
+    } else {
+#pragma unroll
+      for (int t = 0; t < KP; ++t) {
+        a[j][t] = src[((2 * j) * 256 + lane) * KP + t];
+        b[j][t] = src[((2 * j + 1) * 256 + lane) * KP + t];
+      }
+    }
+  }
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = f32x16{};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[j] = M::mma(a[j], b[j], acc[j]);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sum += acc[j][r];
+  out[(int64_t)blockIdx.x * 256 + lane] = sum;
+}
+
+hipError_t launch_debug_mfma_rate(int variant, const void* src, float* out, int iters, int workgroups,
+                                  hipStream_t st) {
+  const dim3 grid(workgroups), block(256);
+  if (variant == 0)
+    hipLaunchKernelGGL(debug_mfma_rate_kernel<f16>, grid, block, 0, st, (const f16*)src, out, iters);
+  else if (variant == 1)
+    hipLaunchKernelGGL(debug_mfma_rate_kernel<bf16>, grid, block, 0, st, (const bf16*)src, out, iters);
+  else
+    hipLaunchKernelGGL(debug_mfma_rate_kernel<float>, grid, block, 0, st, (const float*)src, out, iters);
+  return hipGetLastError();
+}
+
 }  // namespace elsa

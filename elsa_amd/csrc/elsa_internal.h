@@ -108,6 +108,8 @@ int dbias_splits(int N, int batch, int heads, int bias_batch, int bias_heads);
 hipError_t launch_dbias(const BwdParams& p, float* dbias, int bias_batch, int bias_heads, int dtype, int nsplit,
                         float* part, hipStream_t stream);
 hipError_t launch_debug_mfma(int variant, const void* a, const void* b, float* d, hipStream_t stream);
+hipError_t launch_debug_mfma_rate(int variant, const void* src, float* out, int iters, int workgroups,
+                                  hipStream_t stream);
 // dbias[bb', hb'] = sum over the (b, h) pairs broadcast onto it of ds[b, h], in a fixed order;
 // with part (dbias_sum_splits * bias_batch * bias_heads * N * N floats) the pairs are summed in
 // ranges across workgroups and the ranges added in order.

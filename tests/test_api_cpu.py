@@ -166,6 +166,10 @@ def test_bwd_and_dbias_reject_bad_args_without_launching():
     assert lib.elsa_dbias_workspace_bytes(ctypes.byref(b), 0, 1) == 0
     assert lib.elsa_dbias(ctypes.byref(b), 1, 2, 1, None) == _lib.ELSA_ERR_INVALID  # bias_batch 2 vs B=1
     assert lib.elsa_debug_mfma(5, 1, 1, 1, None) == _lib.ELSA_ERR_INVALID
+    assert lib.elsa_debug_mfma_rate(3, 1, 1, 10, 1, None) == _lib.ELSA_ERR_INVALID
+    assert lib.elsa_debug_mfma_rate(0, 1, 1, 0, 1, None) == _lib.ELSA_ERR_INVALID
+    assert lib.elsa_debug_mfma_rate(0, 1, 1, 10, 0, None) == _lib.ELSA_ERR_INVALID
+    assert lib.elsa_debug_mfma_rate(0, None, 1, 10, 1, None) == _lib.ELSA_ERR_INVALID
 
 
 def test_bwd_dbias_rejects_bad_args_and_sizes_its_workspace():
