@@ -137,6 +137,61 @@ def test_dbias_causal_matches_closed_form():
     assert max_abs(host(db), edb) <= 1e-6
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_dbias_beyond_the_reference_dense_limit(causal):
+    """B*H*N^2 above the 64M elements where the reference's dense fallback raises
+    NotImplementedError (attention_bwd.py:923-924): both dbias routes (the training call's
+    dS store and the separate recompute kernel) against the closed form on sampled rows, and
+    the sum of every full row against its closed form."""
+    b, h, n, d = 1, 2, 5800, 64
+    assert b * h * n * n > 64 * 1024 * 1024
+    describe(f"dbias beyond 64M elements causal={causal}")
+    q, k, v, do = O.make_inputs((b, h, n, d), seed=33, dtype="fp16", with_dout=True, dout_scale=0.1)
+    bias = (np.random.default_rng(33).standard_normal((h, n, n)) * 0.3).astype(np.float32)
+    qt, kt, vt = (dev(x, "fp16").requires_grad_(True) for x in (q, k, v))
+    bt = dev(bias, "fp32").requires_grad_(True)
+    out = elsa_amd.twopass_attention_train(qt, kt, vt, bias=bt, is_causal=causal)
+    out.backward(dev(do, "fp16"))
+    with torch.no_grad():
+        o2, rm, rz = elsa_amd.twopass_attention_with_state(qt.detach(), kt.detach(), vt.detach(), bias=bt.detach(),
+                                                           is_causal=causal)
+        db2 = _dense_bias_backward(qt.detach(), kt.detach(), vt.detach(), o2, dev(do, "fp16"), bias=bt.detach(),
+                                   is_causal=causal, row_m=rm, row_z=rz)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(1).choice(n, 12, replace=False))
+    qf, kf, vf, dof = (np.asarray(x, np.float64) for x in (q, k, v, do))
+    # D = rowsum(dO * out) with the stored fp16 output, as the reference's preprocess forms it
+    # (attention_bwd.py:188-224).  Each full row of dS then sums to
+    # sum_j p_ij dp_ij - D_i = dO_i . (out_exact_i - out_i): the closed form on every row.
+    o16 = host(o2)
+    dd = (dof * o16).sum(-1)
+    o_exact = np.empty_like(o16)
+    for hi in range(h):
+        for r0 in range(0, n, 512):
+            r = np.arange(r0, min(n, r0 + 512))
+            s = qf[0, hi, r] @ kf[0, hi].T / np.sqrt(d) + bias[hi, r].astype(np.float64)
+            if causal:
+                s = np.where(np.arange(n)[None, :] <= r[:, None], s, -np.inf)
+            p = np.exp(s - s.max(-1, keepdims=True))
+            o_exact[0, hi, r] = (p / p.sum(-1, keepdims=True)) @ vf[0, hi]
+    row_sum = (dof * (o_exact - o16)).sum(-1)[0]
+    for name, got in (("train", bt.grad), ("dense", db2)):
+        g = host(got)
+        assert g.shape == (h, n, n)
+        assert (np.abs(g.sum(-1) - row_sum) <= 1e-3 * np.abs(g).sum(-1) + 1e-6).all(), name
+        for hi in range(h):
+            s = qf[0, hi, rows] @ kf[0, hi].T / np.sqrt(d) + bias[hi, rows].astype(np.float64)
+            if causal:
+                s = np.where(np.arange(n)[None, :] <= rows[:, None], s, -np.inf)
+            p = np.exp(s - s.max(-1, keepdims=True))
+            p /= p.sum(-1, keepdims=True)
+            dp = dof[0, hi, rows] @ vf[0, hi].T
+            ds = p * (dp - dd[0, hi, rows][:, None])
+            # the same fp16 inputs and D: what remains is fp32 arithmetic, far below 0.1% of
+            # the largest entry
+            assert np.abs(g[hi, rows] - ds).max() <= 1e-3 * np.abs(ds).max(), (name, hi)
+
+
 @pytest.mark.parametrize("bias_shape", [(1, 3, 49, 49), (49, 49)])
 def test_dbias_split_reduction_matches_unsplit_and_closed_form(bias_shape):
     """Swin-like shape (many windows folded into each bias entry): the reduction over the
