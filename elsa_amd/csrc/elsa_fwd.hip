@@ -133,9 +133,14 @@ __device__ inline void store4(void* base, int64_t off, int dtype, float a, float
   }
 }
 
+// The finalize's normaliser: out = s * (1 / z), with one correctly rounded reciprocal per row
+// (0 when z == 0: a row without a valid key has s = 0 and gets out = 0).  Phase 2 and the
+// fused single-partition epilogue both use it, so the two give the same bits.
+__device__ inline float inv_z(float z) { return z > 0.f ? 1.f / z : 0.f; }
+
 // Epilogue of one row of one partition: the summary (m, z, s) for Phase 2, or, when the
 // partition is the whole row (p.direct), Phase 2's finalize in place: s rounded to the
-// summary dtype as the summary store would round it, out = s / z (0 when z == 0), and the
+// summary dtype as the summary store would round it, out = s * inv_z(z), and the
 // row state (m, z) -- the values Phase 2 computes for a single partition.
 __device__ inline float round_to(int dtype, float x) {
   if (dtype == ELSA_F16) return static_cast<float>(static_cast<f16>(x));
@@ -160,9 +165,10 @@ __device__ inline void emit4(const Phase1Params& p, int64_t ridx, int64_t ooff, 
   }
   typedef T t4 __attribute__((ext_vector_type(4)));
   const float v[4] = {a, b, c, e};
+  const float iz = inv_z(z);
   t4 o;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = static_cast<T>(z > 0.f ? round_to(p.s_dtype, v[i]) / z : 0.f);
+  for (int i = 0; i < 4; ++i) o[i] = static_cast<T>(round_to(p.s_dtype, v[i]) * iz);
   *reinterpret_cast<t4*>(static_cast<T*>(p.out) + ooff + d) = o;
 }
 
@@ -721,6 +727,45 @@ __device__ inline void mono_merge(float ma, float za, const float (&sa)[8], floa
   mo = z > 0.f ? m : kNegInf;
 }
 
+// Phase 2 for a non-causal call with exactly NP partitions (2, 4 or 8): every leaf is live,
+// so the loads are unconditional and the up-sweep is the generic kernel's with n = NP
+// (the same merges in the same order: bit-identical results).
+template <typename ST, typename TO, int NP>
+__global__ __launch_bounds__(256) void phase2_np_kernel(const Phase2Params p) {
+  static_assert(NP == 2 || NP == 4 || NP == 8, "power-of-two leaf count");
+  const int cpr = p.D >> 3;
+  const int lid = blockIdx.x * 256 + threadIdx.x, bh = blockIdx.y;
+  if (lid >= p.q_len * cpr) return;
+  const int r = lid / cpr, ch = lid - r * cpr;
+  const int row = p.q_start + r;
+  const int64_t idx0 = (int64_t)bh * p.rows_pad + r, pstride = (int64_t)p.BH * p.rows_pad;
+  float m[NP], z[NP], sv[NP][8];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int64_t idx = idx0 + i * pstride;
+    m[i] = p.m_buf[idx];
+    z[i] = p.z_buf[idx];
+    load8<ST>(p.s_buf, idx * p.D + ch * 8, sv[i]);
+  }
+#pragma unroll
+  for (int w = NP / 2; w >= 1; w >>= 1)
+#pragma unroll
+    for (int i = 0; i < w; ++i)
+      mono_merge(m[2 * i], z[2 * i], sv[2 * i], m[2 * i + 1], z[2 * i + 1], sv[2 * i + 1], m[i], z[i], sv[i]);
+  const int bi = bh / p.H, hi = bh - bi * p.H;
+  TO* out = static_cast<TO*>(p.out) + bi * p.os[0] + hi * p.os[1] + (int64_t)row * p.os[2] + ch * 8;
+  typedef TO o8 __attribute__((ext_vector_type(8)));
+  o8 ov;
+  const float iz = inv_z(z[0]);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) ov[t] = static_cast<TO>(sv[0][t] * iz);
+  *reinterpret_cast<o8*>(out) = ov;
+  if (p.row_m != nullptr && ch == 0) {
+    p.row_m[(int64_t)bh * p.N + row] = z[0] > 0.f ? m[0] : kNegInf;
+    p.row_z[(int64_t)bh * p.N + row] = z[0];
+  }
+}
+
 template <typename ST, typename TO>
 // Grid: x = block of 256 (row, 8-column chunk) pairs of one (batch, head), y = batch * head.
 __global__ __launch_bounds__(256) void phase2_kernel(const Phase2Params p) {
@@ -786,8 +831,9 @@ __global__ __launch_bounds__(256) void phase2_kernel(const Phase2Params p) {
   TO* out = static_cast<TO*>(p.out) + bi * p.os[0] + hi * p.os[1] + (int64_t)row * p.os[2] + ch * 8;
   typedef TO o8 __attribute__((ext_vector_type(8)));
   o8 ov;
+  const float iz = inv_z(az);
 #pragma unroll
-  for (int t = 0; t < 8; ++t) ov[t] = static_cast<TO>(az > 0.f ? as[t] / az : 0.f);
+  for (int t = 0; t < 8; ++t) ov[t] = static_cast<TO>(as[t] * iz);
   *reinterpret_cast<o8*>(out) = ov;
   if (p.row_m != nullptr && ch == 0) {
     p.row_m[(int64_t)bh * p.N + row] = az > 0.f ? am : kNegInf;
@@ -881,7 +927,14 @@ hipError_t launch_phase1(const Phase1Params& p, int dtype, int block_m, hipStrea
 template <typename ST, typename TO>
 static hipError_t launch2(const Phase2Params& p, hipStream_t st) {
   const dim3 grid((unsigned)((p.q_len * (p.D >> 3) + 255) / 256), (unsigned)p.BH);
-  hipLaunchKernelGGL((phase2_kernel<ST, TO>), grid, dim3(256), 0, st, p);
+  if (!p.causal && p.P == 2)
+    hipLaunchKernelGGL((phase2_np_kernel<ST, TO, 2>), grid, dim3(256), 0, st, p);
+  else if (!p.causal && p.P == 4)
+    hipLaunchKernelGGL((phase2_np_kernel<ST, TO, 4>), grid, dim3(256), 0, st, p);
+  else if (!p.causal && p.P == 8)
+    hipLaunchKernelGGL((phase2_np_kernel<ST, TO, 8>), grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((phase2_kernel<ST, TO>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
 
