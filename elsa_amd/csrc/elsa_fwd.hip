@@ -19,8 +19,9 @@
 // Hillis-Steele / finalize kernels, attention_parallel_scan.py:13-120, :375-415):
 //   one thread = one row x 8 head-dim elements; partition summaries are merged
 //   pairwise level by level in registers (Blelloch up-sweep order with identity
-//   padding, groups of 8 partitions), then out = s/z with the z>0 guard and the
-//   base-2 row state is stored.  For causal attention only partitions that start
+//   padding, groups of 8 partitions; up to 8 partitions with the leaf count fixed
+//   at compile time), then out = s * (1/z) with the z>0 guard and the base-2 row
+//   state is stored.  For causal attention only partitions that start
 //   at or before the row are read: later ones are the identity, so this is the
 //   inclusive prefix at the row's own partition (the value the reference's
 //   Hillis-Steele scan hands to its finalize, attention_parallel_scan.py:745).
@@ -727,10 +728,12 @@ __device__ inline void mono_merge(float ma, float za, const float (&sa)[8], floa
   mo = z > 0.f ? m : kNegInf;
 }
 
-// Phase 2 for a non-causal call with exactly NP partitions (2, 4 or 8): every leaf is live,
-// so the loads are unconditional and the up-sweep is the generic kernel's with n = NP
-// (the same merges in the same order: bit-identical results).
-template <typename ST, typename TO, int NP>
+// Phase 2 for calls with at most NP partitions (NP = 2, 4 or 8).  A row merges its live
+// leaves n = P (non-causal) or min(P, row / part_len + 1) (causal: the partitions at or below
+// the row's own) with the generic kernel's up-sweep: the same merges in the same order, and a
+// pair whose right leaf is past n copies its left one.  FULL (non-causal, P == NP): every
+// leaf is live, so the loads are unconditional.
+template <typename ST, typename TO, int NP, bool FULL>
 __global__ __launch_bounds__(256) void phase2_np_kernel(const Phase2Params p) {
   static_assert(NP == 2 || NP == 4 || NP == 8, "power-of-two leaf count");
   const int cpr = p.D >> 3;
@@ -738,20 +741,34 @@ __global__ __launch_bounds__(256) void phase2_np_kernel(const Phase2Params p) {
   if (lid >= p.q_len * cpr) return;
   const int r = lid / cpr, ch = lid - r * cpr;
   const int row = p.q_start + r;
+  int n = NP;
+  if constexpr (!FULL) n = p.causal ? min(p.P, row / p.part_len + 1) : p.P;
   const int64_t idx0 = (int64_t)bh * p.rows_pad + r, pstride = (int64_t)p.BH * p.rows_pad;
   float m[NP], z[NP], sv[NP][8];
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
-    const int64_t idx = idx0 + i * pstride;
-    m[i] = p.m_buf[idx];
-    z[i] = p.z_buf[idx];
-    load8<ST>(p.s_buf, idx * p.D + ch * 8, sv[i]);
+    if (FULL || i < n) {
+      const int64_t idx = idx0 + i * pstride;
+      m[i] = p.m_buf[idx];
+      z[i] = p.z_buf[idx];
+      load8<ST>(p.s_buf, idx * p.D + ch * 8, sv[i]);
+    }
   }
 #pragma unroll
-  for (int w = NP / 2; w >= 1; w >>= 1)
+  for (int w = NP / 2; w >= 1; w >>= 1) {
 #pragma unroll
-    for (int i = 0; i < w; ++i)
-      mono_merge(m[2 * i], z[2 * i], sv[2 * i], m[2 * i + 1], z[2 * i + 1], sv[2 * i + 1], m[i], z[i], sv[i]);
+    for (int i = 0; i < w; ++i) {
+      if (FULL || 2 * i + 1 < n) {
+        mono_merge(m[2 * i], z[2 * i], sv[2 * i], m[2 * i + 1], z[2 * i + 1], sv[2 * i + 1], m[i], z[i], sv[i]);
+      } else if (2 * i < n) {
+        m[i] = m[2 * i];
+        z[i] = z[2 * i];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) sv[i][t] = sv[2 * i][t];
+      }
+    }
+    if constexpr (!FULL) n = (n + 1) >> 1;
+  }
   const int bi = bh / p.H, hi = bh - bi * p.H;
   TO* out = static_cast<TO*>(p.out) + bi * p.os[0] + hi * p.os[1] + (int64_t)row * p.os[2] + ch * 8;
   typedef TO o8 __attribute__((ext_vector_type(8)));
@@ -927,12 +944,19 @@ hipError_t launch_phase1(const Phase1Params& p, int dtype, int block_m, hipStrea
 template <typename ST, typename TO>
 static hipError_t launch2(const Phase2Params& p, hipStream_t st) {
   const dim3 grid((unsigned)((p.q_len * (p.D >> 3) + 255) / 256), (unsigned)p.BH);
-  if (!p.causal && p.P == 2)
-    hipLaunchKernelGGL((phase2_np_kernel<ST, TO, 2>), grid, dim3(256), 0, st, p);
-  else if (!p.causal && p.P == 4)
-    hipLaunchKernelGGL((phase2_np_kernel<ST, TO, 4>), grid, dim3(256), 0, st, p);
-  else if (!p.causal && p.P == 8)
-    hipLaunchKernelGGL((phase2_np_kernel<ST, TO, 8>), grid, dim3(256), 0, st, p);
+  const bool full = !p.causal;
+  if (full && p.P == 2)
+    hipLaunchKernelGGL((phase2_np_kernel<ST, TO, 2, true>), grid, dim3(256), 0, st, p);
+  else if (full && p.P == 4)
+    hipLaunchKernelGGL((phase2_np_kernel<ST, TO, 4, true>), grid, dim3(256), 0, st, p);
+  else if (full && p.P == 8)
+    hipLaunchKernelGGL((phase2_np_kernel<ST, TO, 8, true>), grid, dim3(256), 0, st, p);
+  else if (p.P == 2)
+    hipLaunchKernelGGL((phase2_np_kernel<ST, TO, 2, false>), grid, dim3(256), 0, st, p);
+  else if (p.P >= 3 && p.P <= 4)
+    hipLaunchKernelGGL((phase2_np_kernel<ST, TO, 4, false>), grid, dim3(256), 0, st, p);
+  else if (p.P >= 5 && p.P <= 8)
+    hipLaunchKernelGGL((phase2_np_kernel<ST, TO, 8, false>), grid, dim3(256), 0, st, p);
   else
     hipLaunchKernelGGL((phase2_kernel<ST, TO>), grid, dim3(256), 0, st, p);
   return hipGetLastError();
