@@ -182,6 +182,27 @@ def test_two_pass_structure(causal):
     assert torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("parts", [2, 3, 4, 5, 7, 8, 9, 17])
+def test_phase2_every_partition_count(parts, causal):
+    """Phase 2 over P partitions: the fixed-leaf kernel up to 8 (all leaves live, or a causal
+    row's leading ones), the generic one beyond; both against the oracle's Blelloch up-sweep
+    and the closed form."""
+    n = 1000
+    bn = -(-n // parts)
+    describe(f"phase2 P={parts} block_n={bn} causal={causal}")
+    q, k, v = O.make_inputs((1, 2, n, 64), seed=40 + parts, dtype="fp16")
+    out, rm, rz, *_, plan = two_pass_explicit(dev(q, "fp16"), dev(k, "fp16"), dev(v, "fp16"), is_causal=causal,
+                                              block_n=bn)
+    torch.cuda.synchronize()
+    assert plan["partitions"] == parts
+    eo, em, ez = O.exact_forward(np.float32(q), np.float32(k), np.float32(v), is_causal=causal)
+    ro, rmo, _ = O.forward(q, k, v, is_causal=causal, part_len=bn, dtype="fp16", mode="ref", merge_kind="tree")
+    assert_parity(host(out), eo, ro, FWD_TOL["fp16"], "out", "fp16")
+    assert np.abs(host(rm) - rmo).max() <= 1e-4 * max(1.0, np.abs(rmo).max())
+    np.testing.assert_allclose(host(rz), ez, rtol=2e-3)
+
+
 def test_north_star_shape_properties():
     """B1 H8 d64 N16384 fp16: closed form on sampled rows, a permutation of the keys leaves
     the output unchanged (monoid order invariance) and partitions 2/8 agree."""
