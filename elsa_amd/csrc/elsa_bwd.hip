@@ -722,9 +722,11 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
     qoff[i] = r * (int32_t)p.qs[2] + d0;
     goff[i] = r * (int32_t)p.gs[2] + d0;
   });
-  Chunk16 qreg[NCH], greg[NCH];
-  float lreg = 0.f, dreg = 0.f;
-  auto gload = [&](int t0) {
+  // staging registers: set S holds one 64-row stage on its way from global memory to LDS
+  Chunk16 qreg[2][NCH], greg[2][NCH];
+  float lreg[2] = {0.f, 0.f}, dreg[2] = {0.f, 0.f};
+  auto gload = [&](int t0, auto SET) {
+    constexpr int S = decltype(SET)::value;
     const T* qt = Q + (int64_t)t0 * p.qs[2];
     const T* gt = dO + (int64_t)t0 * p.gs[2];
 static_for<0, NCH>([&](auto I) {
@@ -732,43 +734,38 @@ static_for<0, NCH>([&](auto I) {
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
       if (t0 + r < p.N && d0 < p.D) {
-        qreg[i] = *reinterpret_cast<const Chunk16*>(qt + qoff[i]);
-        greg[i] = *reinterpret_cast<const Chunk16*>(gt + goff[i]);
+        qreg[S][i] = *reinterpret_cast<const Chunk16*>(qt + qoff[i]);
+        greg[S][i] = *reinterpret_cast<const Chunk16*>(gt + goff[i]);
       } else {
-        qreg[i] = Chunk16{};
-        greg[i] = Chunk16{};
+        qreg[S][i] = Chunk16{};
+        greg[S][i] = Chunk16{};
       }
     });
     if (tid < RTS) {  // rows past N: LSE2 = +inf makes their p exactly 0
       const int ra = t0 + tid;
-      lreg = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : __builtin_huge_valf();
-      dreg = ra < p.N ? -p.d_row[(int64_t)bh * p.N + ra] : 0.f;
+      lreg[S] = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : __builtin_huge_valf();
+      dreg[S] = ra < p.N ? -p.d_row[(int64_t)bh * p.N + ra] : 0.f;
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf, auto SET) {
+    constexpr int S = decltype(SET)::value;
 static_for<0, NCH>([&](auto I) {
       constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
-      *reinterpret_cast<Chunk16*>(&Qs[buf][r * KS + d0]) = qreg[i];
-      *reinterpret_cast<Chunk16*>(&Gs[buf][r * KS + d0]) = greg[i];
+      *reinterpret_cast<Chunk16*>(&Qs[buf][r * KS + d0]) = qreg[S][i];
+      *reinterpret_cast<Chunk16*>(&Gs[buf][r * KS + d0]) = greg[S][i];
     });
     if (tid < RTS) {
-      lse_s[buf][tid] = lreg;
-      ndd_s[buf][tid] = dreg;
+      lse_s[buf][tid] = lreg[S];
+      ndd_s[buf][tid] = dreg[S];
     }
   };
 
   const int r_begin = p.causal ? (wg_key0 / RTS) * RTS : 0;
   const int ntiles = (p.N - r_begin + RTS - 1) / RTS;
-  gload(r_begin);
-  sstore(0);
-  __syncthreads();
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
-    const int t0 = r_begin + it * RTS;
-    const bool has_next = it + 1 < ntiles;
-    if (has_next) gload(t0 + RTS);
+  // stage rows [t0, t0 + RTS) from LDS buffer buf into the dK / dV accumulators
+  auto compute = [&](int buf, int t0) __attribute__((always_inline)) {
     if (!p.causal || t0 + RTS - 1 >= key0) {
       const T* qs = Qs[buf];
       const T* gs = Gs[buf];
@@ -864,8 +861,26 @@ static_for<0, NCH>([&](auto I) {
         }
       }
     }
-    if (has_next) sstore(buf ^ 1);
+  };
+  const auto S0 = std::integral_constant<int, 0>{};
+  const auto S1 = std::integral_constant<int, 1>{};
+  // global loads two stages ahead: stage it + 2 goes into the register set that stage it
+  // left, while stage it + 1 waits in the other one for the end of this stage
+  gload(r_begin, S0);
+  sstore(0, S0);
+  if (ntiles > 1) gload(r_begin + RTS, S1);
+  __syncthreads();
+  auto step = [&](int it, auto NEXT, auto FREE) __attribute__((always_inline)) {
+    const int buf = it & 1;
+    const int t0 = r_begin + it * RTS;
+    if (it + 2 < ntiles) gload(t0 + 2 * RTS, FREE);
+    compute(buf, t0);
+    if (it + 1 < ntiles) sstore(buf ^ 1, NEXT);
     __syncthreads();
+  };
+  for (int it = 0; it < ntiles; it += 2) {
+    step(it, S1, S0);
+    if (it + 1 < ntiles) step(it + 1, S0, S1);
   }
 #pragma unroll
   for (int kt = 0; kt < KRT; ++kt) {
