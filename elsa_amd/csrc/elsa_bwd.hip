@@ -527,8 +527,10 @@ void bwd_dq_half_kernel(const BwdParams p) {
     koff[i] = r * (int32_t)p.ks[2] + d0;
     voff[i] = r * (int32_t)p.vs[2] + d0;
   });
-  Chunk16 kreg[NCH], vreg[NCH];
-  auto gload = [&](int t0) {
+  // staging registers: set S holds one 64-key stage on its way from global memory to LDS
+  Chunk16 kreg[2][NCH], vreg[2][NCH];
+  auto gload = [&](int t0, auto SET) {
+    constexpr int S = decltype(SET)::value;
     const T* kt = K + (int64_t)t0 * p.ks[2];
     const T* vt = V + (int64_t)t0 * p.vs[2];
 static_for<0, NCH>([&](auto I) {
@@ -536,21 +538,22 @@ static_for<0, NCH>([&](auto I) {
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
       if (t0 + r < k_end && d0 < p.D) {
-        kreg[i] = *reinterpret_cast<const Chunk16*>(kt + koff[i]);
-        vreg[i] = *reinterpret_cast<const Chunk16*>(vt + voff[i]);
+        kreg[S][i] = *reinterpret_cast<const Chunk16*>(kt + koff[i]);
+        vreg[S][i] = *reinterpret_cast<const Chunk16*>(vt + voff[i]);
       } else {
-        kreg[i] = Chunk16{};
-        vreg[i] = Chunk16{};
+        kreg[S][i] = Chunk16{};
+        vreg[S][i] = Chunk16{};
       }
     });
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf, auto SET) {
+    constexpr int S = decltype(SET)::value;
 static_for<0, NCH>([&](auto I) {
       constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
-      *reinterpret_cast<Chunk16*>(&Ks[buf][r * KS + d0]) = kreg[i];
-      *reinterpret_cast<Chunk16*>(&Vs[buf][r * KS + d0]) = vreg[i];
+      *reinterpret_cast<Chunk16*>(&Ks[buf][r * KS + d0]) = kreg[S][i];
+      *reinterpret_cast<Chunk16*>(&Vs[buf][r * KS + d0]) = vreg[S][i];
     });
   };
 
@@ -561,14 +564,8 @@ static_for<0, NCH>([&](auto I) {
     for (int dt = 0; dt < NDT; ++dt) acc[rt][dt] = f32x16{};
 
   const int ntiles = (k_end + KT - 1) / KT;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
-    const int t0 = it * KT;
-    const bool has_next = it + 1 < ntiles;
-    if (has_next) gload(t0 + KT);
+  // stage keys [t0, t0 + KT) from LDS buffer buf into the dQ accumulators
+  auto compute = [&](int buf, int t0) __attribute__((always_inline)) {
     if (!p.causal || t0 <= row0 + ROWS_W - 1) {
       const T* ks = Ks[buf];
       const T* vs = Vs[buf];
@@ -634,8 +631,42 @@ static_for<0, NCH>([&](auto I) {
         }
       }
     }
-    if (has_next) sstore(buf ^ 1);
+  };
+  const auto S0 = std::integral_constant<int, 0>{};
+  const auto S1 = std::integral_constant<int, 1>{};
+  if constexpr (DP <= 64) {
+    // global loads two stages ahead (as in dK/dV; 16K d64: 0.857 -> 0.842 ms).  At D = 128 the
+    // second register set spills at two waves per SIMD, and one wave per SIMD is slower still
+    // (1.64 against 1.87-2.07 ms), so that width keeps one stage of prefetch
+    gload(0, S0);
+    sstore(0, S0);
+    if (ntiles > 1) gload(KT, S1);
     __syncthreads();
+    auto step = [&](int it, auto NEXT, auto FREE) __attribute__((always_inline)) {
+      const int buf = it & 1;
+      const int t0 = it * KT;
+      if (it + 2 < ntiles) gload(t0 + 2 * KT, FREE);
+      compute(buf, t0);
+      if (it + 1 < ntiles) sstore(buf ^ 1, NEXT);
+      __syncthreads();
+    };
+    for (int it = 0; it < ntiles; it += 2) {
+      step(it, S1, S0);
+      if (it + 1 < ntiles) step(it + 1, S0, S1);
+    }
+  } else {
+    gload(0, S0);
+    sstore(0, S0);
+    __syncthreads();
+    for (int it = 0; it < ntiles; ++it) {
+      const int buf = it & 1;
+      const int t0 = it * KT;
+      const bool has_next = it + 1 < ntiles;
+      if (has_next) gload(t0 + KT, S0);
+      compute(buf, t0);
+      if (has_next) sstore(buf ^ 1, S0);
+      __syncthreads();
+    }
   }
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
