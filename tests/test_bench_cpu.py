@@ -66,6 +66,23 @@ def test_traffic_calibration_needs_the_copy_kernel(tmp_path):
         bench.summarize_pmc(str(tmp_path / "f.csv"), str(tmp_path / "w.csv"), 1024, str(tmp_path / "t.json"))
 
 
+def test_every_elsa_kernel_name_maps_to_its_bench_kernel():
+    """The counter summary recognises each launched kernel by a fragment of its mangled name."""
+    names = {
+        "_ZN4elsa18phase1_half_kernelIDF16_Li64ELi2ELi4ELb0ELb1EEEvNS_12Phase1ParamsE": "phase1_fold",
+        "_ZN4elsa13phase1_kernelIfLi64ELi4ELb0EEEvNS_12Phase1ParamsE": "phase1_fold",
+        "_ZN4elsa16phase2_np_kernelIDF16_DF16_Li2ELb1EEEvNS_12Phase2ParamsE": "phase2_merge",
+        "_ZN4elsa13phase2_kernelIDF16_DF16_EEvNS_12Phase2ParamsE": "phase2_merge",
+        "_ZN4elsa14bwd_pre_kernelIDF16_EEvNS_9BwdParamsE": "bwd_preprocess",
+        "_ZN4elsa18bwd_dq_half_kernelIDF16_Li64ELi1ELi4ELb0EEEvNS_9BwdParamsE": "bwd_dq",
+        "_ZN4elsa13bwd_dq_kernelIfLi64ELi4ELb0EEEvNS_9BwdParamsE": "bwd_dq",
+        "_ZN4elsa20bwd_dkdv_half_kernelIDF16_Li64ELi1ELi4ELb0EEEvNS_9BwdParamsE": "bwd_dkdv",
+        "_ZN4elsa15bwd_dkdv_kernelIfLi64ELi4ELb0EEEvNS_9BwdParamsE": "bwd_dkdv",
+    }
+    for name, key in names.items():
+        assert next(b for frag, b in bench._KERNEL_KEYS if frag in name) == key, name
+
+
 def test_algorithmic_flops():
     assert bench._flops_fwd(1, 8, 16384, 64, False) == 4.0 * 8 * 16384 ** 2 * 64
     assert bench._flops_fwd(1, 1, 4, 2, True) == 4.0 * 2 * (4 * 5 / 2)
