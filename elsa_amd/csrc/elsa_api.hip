@@ -542,6 +542,9 @@ int elsa_debug_mfma_rate(int32_t variant, const void* src, float* out, int32_t i
   if (!src || !out) return fail(ELSA_ERR_INVALID, "null pointer");
   if (iters < 1 || iters > 1000000) return fail(ELSA_ERR_INVALID, "iters must be in [1, 1000000]");
   if (workgroups < 1 || workgroups > 65536) return fail(ELSA_ERR_INVALID, "workgroups must be in [1, 65536]");
+  // bounds one launch to about 2^31 MFMAs (tens of milliseconds)
+  if ((int64_t)iters * workgroups > (int64_t)1 << 26)
+    return fail(ELSA_ERR_INVALID, "iters x workgroups must be at most 2^26");
   hipError_t e = elsa::launch_debug_mfma_rate(variant, src, out, iters, workgroups, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "debug_mfma_rate launch");
   return ELSA_OK;

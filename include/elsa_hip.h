@@ -191,7 +191,8 @@ int elsa_debug_mfma(int32_t variant, const void* a, const void* b, float* d, voi
  * variant 0 fp16 / 1 bf16 (v_mfma_f32_32x32x16, 32768 flop each), 2 fp32 (v_mfma_f32_32x32x2_f32,
  * 4096 flop).  src: [16][256][KP] elements (KP = 8 for 16-bit types, 1 for fp32); out:
  * workgroups * 256 floats.  One launch runs workgroups * 4 waves * iters * 8 MFMAs.
- * iters in [1, 1e6], workgroups in [1, 65536]. */
+ * iters in [1, 1e6], workgroups in [1, 65536], iters x workgroups at most 2^26 (one launch stays within
+ * tens of milliseconds). */
 int elsa_debug_mfma_rate(int32_t variant, const void* src, float* out, int32_t iters, int32_t workgroups,
                          void* stream);
 

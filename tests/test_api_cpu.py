@@ -170,6 +170,7 @@ def test_bwd_and_dbias_reject_bad_args_without_launching():
     assert lib.elsa_debug_mfma_rate(0, 1, 1, 0, 1, None) == _lib.ELSA_ERR_INVALID
     assert lib.elsa_debug_mfma_rate(0, 1, 1, 10, 0, None) == _lib.ELSA_ERR_INVALID
     assert lib.elsa_debug_mfma_rate(0, None, 1, 10, 1, None) == _lib.ELSA_ERR_INVALID
+    assert lib.elsa_debug_mfma_rate(0, 1, 1, 1000000, 65536, None) == _lib.ELSA_ERR_INVALID  # launch too long
 
 
 def test_bwd_dbias_rejects_bad_args_and_sizes_its_workspace():
