@@ -344,6 +344,7 @@ elsa::BwdParams bwd_params(const elsa_bwd_args* a) {
   char* base = static_cast<char*>(a->workspace);
   p.d_row = reinterpret_cast<float*>(base);
   p.lse_row = reinterpret_cast<float*>(base + align256(rows * 4));
+  p.lse_lo = reinterpret_cast<float*>(base + 2 * align256(rows * 4));
   const int H = a->heads, N = a->seq_len, D = a->head_dim;
   resolve_layout(a->q_layout, H, N, D, p.qs);
   resolve_layout(a->k_layout, H, N, D, p.ks);
@@ -413,7 +414,7 @@ int elsa_phase2(const elsa_fwd_args* a, int32_t q_start, int32_t q_len, void* st
 size_t elsa_bwd_workspace_bytes(const elsa_bwd_args* a) {
   if (!a || a->batch <= 0 || a->heads <= 0 || a->seq_len <= 0) return 0;
   const size_t rows = (size_t)a->batch * a->heads * a->seq_len;
-  return 2 * align256(rows * 4);
+  return 3 * align256(rows * 4);  // D, LSE2 and LSE2's low part, one float per row each
 }
 
 int elsa_bwd(const elsa_bwd_args* a, void* stream) { return elsa_bwd_stage(a, -1, stream); }

@@ -159,10 +159,21 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdParams p) {
   if (!ok || sub != 0) return;
   const int64_t i = (int64_t)bh * p.N + row;
   p.d_row[i] = acc;
-  // LSE2 = m + log2(max(z, 1e-30)) (attention_bwd.py:224); a row with no valid key
-  // (z == 0) stores +inf instead of -inf so that p = exp2(s - LSE2) is 0 without a test.
+  // LSE2 = m + log2(max(z, 1e-30)) (attention_bwd.py:224), formed in double and split into
+  // its fp32 rounding and the remainder, so that the fp32 kernels' p = exp2(s*c - LSE2) does
+  // not carry the half-ulp of a ~15-magnitude LSE2 (3e-7 relative, the same for a whole row)
+  // into every gradient of that row.  A row with no valid key (z == 0) stores +inf instead
+  // of -inf so that p is 0 without a test.
   const float z = p.row_z[i];
-  p.lse_row[i] = z > 0.f ? p.row_m[i] + __log2f(fmaxf(z, 1.0e-30f)) : __builtin_huge_valf();
+  if (z > 0.f) {
+    const double l = (double)p.row_m[i] + log2((double)fmaxf(z, 1.0e-30f));
+    const float hi = (float)l;
+    p.lse_row[i] = hi;
+    p.lse_lo[i] = (float)(l - (double)hi);
+  } else {
+    p.lse_row[i] = __builtin_huge_valf();
+    p.lse_lo[i] = 0.f;
+  }
 }
 
 // ------------------------------------------------------------------ dq
@@ -210,6 +221,7 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
     gf[m] = ok ? *reinterpret_cast<const f32x4*>(dO + (int64_t)rsafe * p.gs[2] + d0) : f32x4{};
   }
   const float lse = row_ok ? p.lse_row[(int64_t)bh * p.N + my_row] : 0.f;
+  const float lse_lo = row_ok ? p.lse_lo[(int64_t)bh * p.N + my_row] : 0.f;
   const float dd = row_ok ? p.d_row[(int64_t)bh * p.N + my_row] : 0.f;
   const bool live = row_ok && lse > kNegInf;
 
@@ -256,11 +268,18 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
       const int key = t0 + key_of_reg(r, g);
       bool ok = live;
       if (!full) ok = ok && key < k_end && (!p.causal || key <= my_row);
-      float x = s[r] * p.scale_log2;
+      // s*c - LSE2 with one rounding of the (small) difference, then LSE2's low part
+      float x = fmaf(s[r], p.scale_log2, -lse) - lse_lo;
       if constexpr (HAS_BIAS) x = ok ? fmaf(load_bias_b(p.bias, bi, hi, my_row, key), kLog2e, x) : x;
-      const float pr = ok ? fast_exp2(x - lse) : 0.f;
+      const float pr = ok ? fast_exp2(x) : 0.f;
       s[r] = pr * (dp[r] - dd);
     }
+    // this stage's 32 keys into a fresh accumulator, then one add into the running sum: each
+    // dq element is a chain of N/32 adds plus 16 MFMA steps, not N/2 MFMA steps (B8 H3 N1025:
+    // 1.06e-6 from the exact dq against the 1e-6 bar, sequential over 513 steps)
+    f32x16 st[C::NDT];
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; ++dt) st[dt] = f32x16{};
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
       const int k0 = 16 * (jb >> 1) + 8 * g + 4 * (jb & 1);  // key_of_reg(4 jb, g)
@@ -268,9 +287,11 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
       for (int dt = 0; dt < C::NDT; ++dt) {
         const float* ka = Kt + (dt * 32 + c) * TS1 + k0;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[dt] = M::mma(ka[u], s[4 * jb + u], acc[dt]);
+        for (int u = 0; u < 4; ++u) st[dt] = M::mma(ka[u], s[4 * jb + u], st[dt]);
       }
     }
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; ++dt) acc[dt] += st[dt];
   }
   if (!row_ok) return;
   T* out = static_cast<T*>(p.dq) + bi * p.dqs[0] + hi * p.dqs[1] + (int64_t)my_row * p.dqs[2];
@@ -308,7 +329,7 @@ void bwd_dkdv_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) float Gt[2][DP * TS1];
   __shared__ __attribute__((aligned(16))) float Qr[2][TT * RS4];
   __shared__ __attribute__((aligned(16))) float Gr[2][TT * RS4];
-  __shared__ float lse_s[2][TT], dd_s[2][TT];
+  __shared__ float lse_s[2][TT], lo_s[2][TT], dd_s[2][TT];
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
@@ -343,13 +364,14 @@ void bwd_dkdv_kernel(const BwdParams p) {
   const int r_begin = p.causal ? (wg_key0 / TT) * TT : 0;
   const int ntiles = (p.N - r_begin + TT - 1) / TT;
   Chunk16 qreg[F32Stage<DP, NT>::NCH], greg[F32Stage<DP, NT>::NCH];
-  float lreg = 0.f, dreg = 0.f;
+  float lreg = 0.f, loreg = 0.f, dreg = 0.f;
   auto gload = [&](int t0) {
     f32_stage_load<DP, NT>(qreg, Q, p.qs[2], t0, p.N, p.D, tid);
     f32_stage_load<DP, NT>(greg, dO, p.gs[2], t0, p.N, p.D, tid);
     if (tid < TT) {
       const int ra = t0 + tid;
       lreg = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : kNegInf;
+      loreg = ra < p.N ? p.lse_lo[(int64_t)bh * p.N + ra] : 0.f;
       dreg = ra < p.N ? p.d_row[(int64_t)bh * p.N + ra] : 0.f;
     }
   };
@@ -358,6 +380,7 @@ void bwd_dkdv_kernel(const BwdParams p) {
     f32_stage_store2<DP, NT, F32Stage<DP, NT>::NCH, TS1, RS4>(greg, Gt[buf], Gr[buf], tid);
     if (tid < TT) {
       lse_s[buf][tid] = lreg;
+      lo_s[buf][tid] = loreg;
       dd_s[buf][tid] = dreg;
     }
   };
@@ -395,9 +418,10 @@ void bwd_dkdv_kernel(const BwdParams p) {
       const float lse = lse_s[buf][rl];
       bool ok = key_ok && row < p.N && lse > kNegInf;
       if (p.causal) ok = ok && row >= my_key;
-      float x = s[r] * p.scale_log2;
+      // s*c - LSE2 with one rounding of the (small) difference, then LSE2's low part
+      float x = fmaf(s[r], p.scale_log2, -lse) - lo_s[buf][rl];
       if constexpr (HAS_BIAS) x = ok ? fmaf(load_bias_b(p.bias, bi, hi, row, my_key), kLog2e, x) : x;
-      const float pr = ok ? fast_exp2(x - lse) : 0.f;
+      const float pr = ok ? fast_exp2(x) : 0.f;
       pv[r] = pr;
       s[r] = pr * (dp[r] - dd_s[buf][rl]);
       if constexpr (HAS_BIAS) {
@@ -1043,13 +1067,15 @@ __global__ __launch_bounds__(64) void dbias_kernel(const BwdParams p, float* dbi
         dp = M::mma(va, gb, dp);
       }
       const float lse = row_ok ? p.lse_row[(int64_t)bh * p.N + my_row] : kNegInf;
+      const float lse_lo = row_ok ? p.lse_lo[(int64_t)bh * p.N + my_row] : 0.f;
       const float dd = row_ok ? p.d_row[(int64_t)bh * p.N + my_row] : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = tj * 32 + key_of_reg(r, g);
         bool ok = row_ok && key < p.N && lse > kNegInf && (!p.causal || key <= my_row);
-        const float x = ok ? fmaf(load_bias_b(p.bias, b, h, my_row, key), kLog2e, s[r] * p.scale_log2) : 0.f;
-        const float pr = ok ? fast_exp2(x - lse) : 0.f;
+        // s*c - LSE2 rounded once (then LSE2's low part), before the bias: as the dq and dk/dv kernels
+        const float x = fmaf(s[r], p.scale_log2, -lse) - lse_lo;
+        const float pr = ok ? fast_exp2(fmaf(load_bias_b(p.bias, b, h, my_row, key), kLog2e, x)) : 0.f;
         acc[r] += pr * (dp[r] - dd);
       }
     }

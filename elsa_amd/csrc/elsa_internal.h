@@ -88,7 +88,8 @@ struct BwdParams {
   void* dv;
   BiasView bias;
   float* d_row;    // [BH, N]
-  float* lse_row;  // [BH, N]
+  float* lse_row;  // [BH, N]: LSE2 rounded to fp32
+  float* lse_lo;   // [BH, N]: LSE2 - lse_row (fp32 kernels subtract both: p is exact to fp32 rounding)
   // biased dk/dv kernels: when set, also store dS = p * (dP - D) in fp32, [BH, N, N]
   float* ds_out;
   int H, N, D, BH;

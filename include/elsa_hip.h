@@ -128,7 +128,7 @@ typedef struct elsa_bwd_args {
   int32_t is_causal;
   float scale;           /* softmax scale on q.k; 0 = 1/sqrt(head_dim)          */
   int32_t _pad;
-  void* workspace;       /* 2*B*H*N floats (D and LSE2 rows)                   */
+  void* workspace;       /* 3*B*H*N floats (D, LSE2 and its low part): elsa_bwd_workspace_bytes */
   size_t workspace_bytes;
   /* zero = dense [B,H,N,D].  The reference backward reads contiguous copies
    * (attention_bwd.py:722-726); strided views avoid them. */

@@ -214,6 +214,34 @@ def canonical_bias(bias: Optional[np.ndarray], batch: int, heads: int, n: int) -
 
 
 # --------------------------------------------------------------------------
+# the reference's Phase-1 layout
+# --------------------------------------------------------------------------
+def reference_routing(n: int, d: int, dtype: str, *, training: bool = False, is_causal: bool = False,
+                      has_bias: bool = False) -> tuple:
+    """(part_len, micro): keys per K partition and per fold micro-tile in the reference.
+
+    Partition width ``block_n``: inference ``_paper_scan_defaults`` (attention.py:175-226),
+    training ``twopass_attention_with_state`` (attention_bwd.py:130-158).  The d64 fast
+    path (``_can_use_d64_parallel_final``, attention_parallel_scan.py:418-440, never causal,
+    :983-1018) folds 64-key micro-tiles when ``block_n > 512`` (:467-468) and one
+    ``block_n`` tile otherwise (K3/K4, :123-224); the generic kernel (attention.py:22-106:
+    bias, causal, bf16, D != 64) folds one ``block_n`` tile per program.
+    """
+    if dtype == "fp32":
+        if d <= 64:
+            bn = 256 if n <= 512 else (((n + 63) // 64) * 64 if n < 2048 else 2048)
+        else:
+            bn = 64
+    elif not training and dtype == "fp16" and d == 64 and n >= 8192:
+        bn = 2048
+    else:
+        bn = 256 if d <= 64 else 64
+    fast = not has_bias and not is_causal and d == 64 and dtype in ("fp16", "fp32") and bn % 64 == 0
+    micro = 64 if (fast and bn > 512) else bn
+    return bn, micro
+
+
+# --------------------------------------------------------------------------
 # Phase 1
 # --------------------------------------------------------------------------
 def _scores(q_rows, k_tile, *, dtype: str, mode: str, generic: bool, scale: float, bias_tile, wd):

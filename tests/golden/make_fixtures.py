@@ -65,7 +65,7 @@ def swin_bias(b: int, h: int, n: int, seed: int) -> np.ndarray:
 
 def compute(case):
     shape, dt, causal, part_len, bias_kind, seed = case
-    q, k, v, do = O.make_inputs(shape, seed=seed, dtype=dt, with_dout=True, dout_scale=0.1)
+    q, k, v, do = O.make_inputs(shape, seed=seed, dtype=dt, with_dout=True, dout_scale=1.0)
     bias = swin_bias(shape[0], shape[1], shape[2], seed) if bias_kind == "swin" else None
     out, rm, rz = O.forward(q, k, v, bias=bias, is_causal=causal, part_len=part_len, dtype=dt, mode="ref")
     dq, dk, dv = O.backward(q, k, v, out, do, rm, rz, bias=bias, is_causal=causal, dtype=dt, mode="ref")
@@ -87,7 +87,7 @@ def compute(case):
         rec["dbias"] = O.dbias(qf, kf, vf, out, dof, rm, rz, bias=bias, is_causal=causal).astype(np.float32)
         rec["dbias_exact"] = O.dbias(qf, kf, vf, eo, dof, em, ez, bias=bias, is_causal=causal).astype(ex)
     meta = {"shape": list(shape), "dtype": dt, "causal": causal, "part_len": part_len,
-            "bias": bias_kind, "seed": seed, "dout_scale": 0.1}
+            "bias": bias_kind, "seed": seed, "dout_scale": 1.0}
     rec["meta"] = np.array(json.dumps(meta, sort_keys=True))
     return rec
 

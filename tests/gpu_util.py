@@ -68,3 +68,4 @@ def assert_parity(got, exact, ref, tol: float, what: str = "", dtype: str = "fp1
     assert d_ref <= max(tol, 2.0 * e_ref), (what, info)
     assert e_got <= max(tol, 1.25 * e_ref), (what, info)
     return info
+

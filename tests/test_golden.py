@@ -87,9 +87,11 @@ def test_closed_form_fields_match_math_sdpa(path):
 
 
 # the reference's published error against math SDPA (README.md:31, 78-79): fp32 ~5e-7 forward,
-# ~1e-7 gradients; fp16 ~4-5e-4 forward, ~1.5e-5 gradients.  49-token windows and short causal
-# rows sit above the long-sequence figures because each fp16 rounding of p / dS weighs more.
-REF_ERR = {"fp32": (1e-6, 1e-6), "fp16": (2e-3, 1e-4), "bf16": (2e-2, 1e-3)}
+# ~1e-7 gradients; fp16 ~4-5e-4 forward, ~1.5e-5 gradients.  Its gradient figures are measured
+# with dO scaled by 0.1 (benchmarks/bwd_grad_correctness.py:24); these fixtures draw dO ~ N(0,1),
+# so the gradient errors are ten times larger.  49-token windows and short causal rows sit above
+# the long-sequence figures because each fp16 rounding of p / dS weighs more.
+REF_ERR = {"fp32": (1e-6, 2e-6), "fp16": (2e-3, 1e-3), "bf16": (2e-2, 1e-2)}
 
 
 @pytest.mark.parametrize("path", FILES, ids=IDS)
@@ -153,4 +155,5 @@ def test_hip_path_meets_the_bar_on_the_golden_vectors(path):
     np.testing.assert_allclose(host(row_z), rec["row_z"], rtol=2e-3 if dt != "fp32" else 1e-5)
     if bt is not None:
         # each entry of this [B, H, N, N] bias is one (b, h) pair's dS: the gradient bar applies
-        assert np.abs(host(bt.grad) - rec["dbias_exact"]).max() <= 2 * GRAD_TOL[dt]
+        describe(str(assert_parity(host(bt.grad), rec["dbias_exact"], rec["dbias"], GRAD_TOL[dt], "dbias",
+                                   "fp32")))

@@ -46,7 +46,7 @@ CASES = [
 def test_backward_matches_oracle_and_closed_form(case):
     shape, dt, causal = case
     describe(f"backward {case}")
-    q, k, v, do = O.make_inputs(shape, seed=2026 + shape[2], dtype=dt, with_dout=True, dout_scale=0.1)
+    q, k, v, do = O.make_inputs(shape, seed=2026 + shape[2], dtype=dt, with_dout=True, dout_scale=1.0)
     out, dq, dk, dv = _run_train(q, k, v, do, dt, is_causal=causal)
     qf, kf, vf, dof = (np.asarray(x, np.float32) for x in (q, k, v, do))
     eq, ek, ev, _ = O.exact_backward(qf, kf, vf, dof, is_causal=causal)
@@ -82,7 +82,7 @@ def test_reference_train_test_against_sdpa(dt, causal):
 @pytest.mark.parametrize("dt", ["fp32", "fp16"])
 def test_backward_without_saved_state_uses_row_stats(dt):
     describe(f"backward row-stats {dt}")
-    q, k, v, do = O.make_inputs((1, 2, 333, 64), seed=4, dtype=dt, with_dout=True, dout_scale=0.1)
+    q, k, v, do = O.make_inputs((1, 2, 333, 64), seed=4, dtype=dt, with_dout=True, dout_scale=1.0)
     qd, kd, vd, dod = (dev(x, dt) for x in (q, k, v, do))
     out, rm, rz = elsa_amd.twopass_attention_with_state(qd, kd, vd, is_causal=True)
     g_state = elsa_amd.twopass_attention_backward(qd, kd, vd, out, dod, is_causal=True, row_m=rm, row_z=rz)
@@ -104,7 +104,7 @@ def test_backward_without_saved_state_uses_row_stats(dt):
 def test_bias_gradients(dt, bias_shape):
     describe(f"backward bias {bias_shape} {dt}")
     shape = (4, 3, 49, 32)
-    q, k, v, do = O.make_inputs(shape, seed=9, dtype=dt, with_dout=True, dout_scale=0.1)
+    q, k, v, do = O.make_inputs(shape, seed=9, dtype=dt, with_dout=True, dout_scale=1.0)
     bias = (np.random.default_rng(9).standard_normal(bias_shape) * 0.5).astype(np.float32)
     qt, kt, vt = (dev(x, dt).requires_grad_(True) for x in (q, k, v))
     bt = dev(bias, "fp32").requires_grad_(True)
@@ -122,19 +122,22 @@ def test_bias_gradients(dt, bias_shape):
         assert_parity(host(got), exp, ref, tol, name, dt)
     assert bt.grad.shape == bias.shape
     summed = (shape[0] * shape[1]) // int(np.prod(bias_shape[:-2]))  # (b, h) pairs folded into each entry
-    assert max_abs(host(bt.grad), edb) <= 2 * tol * summed
+    rdb = O.dbias(qf, kf, vf, fo, dof, fm, fz, bias=bias)
+    assert_parity(host(bt.grad), edb, rdb, tol * summed, "dbias", "fp32")
 
 
 def test_dbias_causal_matches_closed_form():
     describe("dbias causal")
-    q, k, v, do = O.make_inputs((2, 2, 70, 32), seed=12, dtype="fp32", with_dout=True, dout_scale=0.1)
+    q, k, v, do = O.make_inputs((2, 2, 70, 32), seed=12, dtype="fp32", with_dout=True, dout_scale=1.0)
     bias = (np.random.default_rng(12).standard_normal((2, 2, 70, 70)) * 0.3).astype(np.float32)
     qd, kd, vd, dod, bd = (dev(x, "fp32") for x in (q, k, v, do, bias))
     out, rm, rz = elsa_amd.twopass_attention_with_state(qd, kd, vd, bias=bd, is_causal=True)
     db = _dense_bias_backward(qd, kd, vd, out, dod, bias=bd, is_causal=True, row_m=rm, row_z=rz)
     eo, em, ez = O.exact_forward(q, k, v, bias=bias, is_causal=True)
     edb = O.dbias(q, k, v, eo, do, em, ez, bias=bias, is_causal=True)
-    assert max_abs(host(db), edb) <= 1e-6
+    fo, fm, fz = O.forward(q, k, v, bias=bias, is_causal=True, dtype="fp32", mode="ref")
+    rdb = O.dbias(q, k, v, fo, do, fm, fz, bias=bias, is_causal=True)
+    describe(str(assert_parity(host(db), edb, rdb, GRAD_TOL["fp32"], "dbias", "fp32")))
 
 
 @pytest.mark.parametrize("causal", [False, True])
@@ -146,7 +149,7 @@ def test_dbias_beyond_the_reference_dense_limit(causal):
     b, h, n, d = 1, 2, 5800, 64
     assert b * h * n * n > 64 * 1024 * 1024
     describe(f"dbias beyond 64M elements causal={causal}")
-    q, k, v, do = O.make_inputs((b, h, n, d), seed=33, dtype="fp16", with_dout=True, dout_scale=0.1)
+    q, k, v, do = O.make_inputs((b, h, n, d), seed=33, dtype="fp16", with_dout=True, dout_scale=1.0)
     bias = (np.random.default_rng(33).standard_normal((h, n, n)) * 0.3).astype(np.float32)
     qt, kt, vt = (dev(x, "fp16").requires_grad_(True) for x in (q, k, v))
     bt = dev(bias, "fp32").requires_grad_(True)
@@ -204,7 +207,7 @@ def test_dbias_split_reduction_matches_unsplit_and_closed_form(bias_shape):
 
     describe(f"dbias split {bias_shape}")
     shape = (64, 3, 49, 32)
-    q, k, v, do = O.make_inputs(shape, seed=21, dtype="fp32", with_dout=True, dout_scale=0.1)
+    q, k, v, do = O.make_inputs(shape, seed=21, dtype="fp32", with_dout=True, dout_scale=1.0)
     bias = (np.random.default_rng(21).standard_normal(bias_shape) * 0.5).astype(np.float32)
     qd, kd, vd, dod, bd = (dev(x, "fp32") for x in (q, k, v, do, bias))
     out, rm, rz = elsa_amd.twopass_attention_with_state(qd, kd, vd, bias=bd)
@@ -227,7 +230,9 @@ def test_dbias_split_reduction_matches_unsplit_and_closed_form(bias_shape):
     _lib.check(lib.elsa_dbias(ctypes.byref(args), unsplit.data_ptr(), bias_b, bias_h, _lib.stream_handle(qd.device)),
                "elsa_dbias")
     torch.cuda.synchronize()
-    np.testing.assert_allclose(host(split).reshape(-1), host(unsplit).reshape(-1), rtol=1e-5, atol=1e-6)
+    # the same fp32 sums in two orders over the 192 broadcast pairs
+    np.testing.assert_allclose(host(split).reshape(-1), host(unsplit).reshape(-1), rtol=1e-5,
+                               atol=1e-6 * (shape[0] * shape[1]) ** 0.5)
 
 
 @pytest.mark.parametrize("dt,n,causal,d", [("fp16", 197, False, 64), ("bf16", 1025, True, 64), ("fp32", 300, False, 64),
@@ -404,7 +409,7 @@ def test_bwd_dbias_matches_bwd_then_dbias(dt, shape, bias_shape, causal):
 
     describe(f"elsa_bwd_dbias {dt} {shape} bias {bias_shape} causal={causal}")
     b, h, n, d = shape
-    q, k, v, do = O.make_inputs(shape, seed=n + d, dtype=dt, with_dout=True, dout_scale=0.3)
+    q, k, v, do = O.make_inputs(shape, seed=n + d, dtype=dt, with_dout=True, dout_scale=1.0)
     bias = (np.random.default_rng(n).standard_normal(bias_shape) * 0.5).astype(np.float32)
     qd, kd, vd, dod = (dev(x, dt) for x in (q, k, v, do))
     bd = dev(bias, dt)
