@@ -8,8 +8,10 @@ d=64 fp16, non-causal, synthetic N(0,1) q/k/v/dO (seed 2026) resident in HBM.
 Prints ONE JSON line.  ``value`` is the algorithmic fwd+bwd throughput
 (3.5 * 4*B*H*N^2*d flop per step, recompute not counted).  ``kernels`` holds each
 kernel's HIP-event average on the launch stream; ``roofline`` is computed for the
-kernel with the largest share of the step.  ``cpu_baseline`` times the numpy
-restatement of the reference algorithm (oracle/) on a bounded row sample.
+kernel with the largest share of the step.  ``cpu_baseline`` times BASELINE config 1
+(B1 H8 N1024 d64 fp32 forward) through the pure-PyTorch restatement of the reference's
+monoid scan (oracle/torch_scan.py) on the host cores, with a row sample of this step's
+own work beside it.
 """
 from __future__ import annotations
 
@@ -48,14 +50,21 @@ def _args():
                          "kernels run the same instructions for all four, which isolates the data-dependent clock")
     ap.add_argument("--cpu-baseline", dest="cpu_baseline", action="store_true", default=True)
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
-    ap.add_argument("--cpu-rows", type=int, default=1536, help="query rows of the CPU-baseline sample")
+    ap.add_argument("--cpu-rows", type=int, default=2048, help="query rows of the north-star CPU sample")
     ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "traffic_north_star.json"))
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after timing, run one copy kernel over this many MiB (HBM-counter calibration)")
-    ap.add_argument("--vit-img", type=int, nargs="*", default=[224, 1024],
-                    help="ViT-Tiny image sizes for the img/s fields (empty: skip)")
-    ap.add_argument("--swin-img", type=int, nargs="*", default=[224],
-                    help="Swin-Tiny image sizes for the img/s fields (empty: skip)")
+    # BASELINE configs 4 and 5: ViT-T at 224/512/1024/2048 px and Swin-T at 224/384/512 px, batch 8
+    ap.add_argument("--vit-img", type=int, nargs="*", default=[224, 512, 1024, 2048],
+                    help="ViT-Tiny image sizes for the img/s fields in --dtype (empty: skip)")
+    ap.add_argument("--swin-img", type=int, nargs="*", default=[224, 384, 512],
+                    help="Swin-Tiny image sizes for the img/s fields in --dtype (empty: skip)")
+    # the same models in fp32 as second fields (ViT up to 1024 px, the sizes of the reference's
+    # fp32 ViT table, README.md:65, 74)
+    ap.add_argument("--vit-img-fp32", type=int, nargs="*", default=[224, 512, 1024],
+                    help="ViT-Tiny image sizes of the fp32 fields (empty: skip)")
+    ap.add_argument("--swin-img-fp32", type=int, nargs="*", default=[224, 384, 512],
+                    help="Swin-Tiny image sizes of the fp32 fields (empty: skip)")
     ap.add_argument("--vit-batch", type=int, default=8, help="image batch of the ViT-T / Swin-T fields")
     ap.add_argument("--vit-steps", type=int, default=10, help="timed iterations of the ViT-T / Swin-T fields")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -365,18 +374,19 @@ def main() -> int:
     }
     if vs_sdpa is not None:
         result["vs_sdpa"] = vs_sdpa
-    if args.vit_img:
-        from elsa_amd.vision_models import vit_tiny_patch16
+    from elsa_amd.vision_models import swin_tiny_patch4_window7, vit_tiny_patch16
 
-        result["vit_tiny"] = _vision_bench(args, dt, vit_tiny_patch16, args.vit_img,
-                                           "vit_tiny_patch16 (embed 192, depth 12, heads 3, d 64), random init",
-                                           lambda img: (img // 16) ** 2 + 1)
-    if args.swin_img:
-        from elsa_amd.vision_models import swin_tiny_patch4_window7
-
-        result["swin_tiny"] = _vision_bench(args, dt, swin_tiny_patch4_window7, args.swin_img,
-                                            "swin_tiny_patch4_window7 (embed 96, depths 2-2-6-2, heads 3-6-12-24, "
-                                            "d 32, window 7), random init", lambda img: 49)
+    vit = ("vit_tiny_patch16 (embed 192, depth 12, heads 3, d 64), random init", lambda img: (img // 16) ** 2 + 1)
+    swin = ("swin_tiny_patch4_window7 (embed 96, depths 2-2-6-2, heads 3-6-12-24, d 32, window 7; feature maps "
+            "padded to whole windows), random init", lambda img: 49)
+    model_runs = [("vit_tiny", dt, vit_tiny_patch16, args.vit_img, vit),
+                  ("swin_tiny", dt, swin_tiny_patch4_window7, args.swin_img, swin)]
+    if dt != torch.float32:
+        model_runs += [("vit_tiny_fp32", torch.float32, vit_tiny_patch16, args.vit_img_fp32, vit),
+                       ("swin_tiny_fp32", torch.float32, swin_tiny_patch4_window7, args.swin_img_fp32, swin)]
+    for key, mdt, builder, imgs, (label, tokens) in model_runs:
+        if imgs:
+            result[key] = _vision_bench(args, mdt, builder, imgs, label, tokens)
     if args.copy_mib > 0:
         # one elementwise kernel that reads and writes copy_mib MiB each: the FETCH_SIZE / WRITE_SIZE
         # calibration for the HBM-traffic figures
@@ -449,7 +459,7 @@ def _vision_bench(args, dt, builder, imgs, label, tokens):
 
     import elsa_amd
 
-    out = {"model": label, "batch": args.vit_batch}
+    out = {"model": label, "batch": args.vit_batch, "dtype": str(dt).replace("torch.", "")}
     for img in imgs:
         torch.manual_seed(2468 + img)
         base = builder(img)
@@ -526,44 +536,106 @@ def _train_ms(model, x, labels, steps):
     return round(e0.elapsed_time(e1) / steps, 4)
 
 
-def _cpu_baseline(args, B, H, N, D, causal):
-    """Time the numpy restatement (oracle/) of the reference algorithm on a row sample."""
-    import numpy as np
-
-    from oracle import elsa_oracle as O
-
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
-    except Exception:  # noqa: BLE001
-        threads = os.cpu_count() or 1
-    rows = np.arange(min(args.cpu_rows, N))
-    q, k, v, do = O.make_inputs((B, H, N, D), seed=2026, dtype=args.dtype, with_dout=True)
-    qs, dos = q[:, :, rows], do[:, :, rows]
-    print(f"bench: cpu baseline on {len(rows)} of {N} query rows, {threads} threads", file=sys.stderr, flush=True)
-    t0 = time.perf_counter()
-    out, rm, rz = O.forward(q, k, v, is_causal=causal, part_len=max(64, N // 2), dtype=args.dtype, mode="ref",
-                            rows=rows)
-    O.backward(qs, k, v, out, dos, rm, rz, is_causal=causal, dtype=args.dtype, mode="ref", rows=rows)
-    secs = time.perf_counter() - t0
-    frac = len(rows) / N
-    flops = 3.5 * _flops_fwd(B, H, N, D, causal) * (frac if not causal else
-                                                   (rows + 1).sum() / (N * (N + 1) / 2))
+def _cpu_model() -> str:
     cpu = platform.processor() or platform.machine()
     try:
         with open("/proc/cpuinfo") as fh:
             for line in fh:
                 if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(flops / secs / 1e12, 5), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
-            "sample": f"numpy restatement (oracle/elsa_oracle.py, reference rounding points) of fwd+bwd for "
-                      f"{len(rows)} of {N} query rows x all {N} keys, B{B} H{H} d{D} {args.dtype}; {secs:.2f} s on "
-                      f"{cpu}, os.cpu_count()={os.cpu_count()}",
-            "seconds": round(secs, 3)}
+    return cpu
+
+
+def _median_s(fn, warmup=3, iters=10):
+    import statistics
+
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def _cpu_baseline(args, B, H, N, D, causal):
+    """The reference algorithm on the host cores, a reported baseline.
+
+    The reference has no CPU path (every entry point rejects non-CUDA tensors,
+    attention.py:268-269), so this times oracle/torch_scan.py, the build's pure-PyTorch
+    restatement of the reference's monoid scan (Phase-1 fold per K partition at the
+    reference's partition and micro-tile widths, the merge, out = s/z), on every thread
+    torch is given (OMP_NUM_THREADS on the GPU box):
+
+    * ``value``: BASELINE config 1 -- non-causal B1 H8 N1024 d64 fp32 forward, q, k, v
+      ~ N(0,1) from torch.Generator seed 1234 in that order, scale 1/8 -- median of 10
+      after 3 warm-ups, checked against math SDPA in float64, with CPU math SDPA timed
+      beside it;
+    * ``north_star_sample``: the benchmarked step's own work (fwd + bwd at the reference's
+      rounding points) for the first query rows of this run's shape.
+    """
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from oracle import elsa_oracle as O
+    from oracle import torch_scan as T
+
+    threads = torch.get_num_threads()
+    cpu = _cpu_model()
+    print(f"bench: cpu baseline (BASELINE config 1) on {threads} threads of {cpu}", file=sys.stderr, flush=True)
+    g = torch.Generator().manual_seed(1234)
+    shape1 = (1, 8, 1024, 64)
+    q1, k1, v1 = (torch.randn(shape1, generator=g) for _ in range(3))
+    part1, micro1 = O.reference_routing(1024, 64, "fp32")
+    res = {}
+
+    def scan():
+        res["out"] = T.forward(q1, k1, v1, part_len=part1, micro=micro1, dtype="fp32")[0]
+
+    secs = _median_s(scan)
+    sdpa_secs = _median_s(lambda: F.scaled_dot_product_attention(q1, k1, v1, scale=0.125))
+    exact = F.scaled_dot_product_attention(q1.double(), k1.double(), v1.double(), scale=0.125)
+    err = float((res["out"].double() - exact).abs().max())
+    f1 = _flops_fwd(*shape1, False)
+    out = {"value": round(f1 / secs / 1e12, 5), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+           "sample": f"BASELINE config 1: non-causal B1 H8 N1024 d64 fp32 forward (seed 1234, scale 1/8) through "
+                     f"oracle/torch_scan.py, the pure-PyTorch restatement of the reference's monoid scan "
+                     f"({part1}-key partition, {micro1}-key micro-tiles); median of 10 after 3 warm-ups: "
+                     f"{secs * 1e3:.2f} ms on {threads} threads of {cpu} (os.cpu_count()={os.cpu_count()})",
+           "ms": round(secs * 1e3, 3), "gflops": round(f1 / secs / 1e9, 2),
+           "max_abs_vs_math_sdpa_fp64": err,
+           "cpu_math_sdpa": {"ms": round(sdpa_secs * 1e3, 3), "gflops": round(f1 / sdpa_secs / 1e9, 2),
+                             "what": "torch.nn.functional.scaled_dot_product_attention on the same fp32 inputs "
+                                     "(CPU math path), for context"},
+           "cpu_model": cpu}
+
+    # the north-star step's own work on a row sample
+    rows = np.arange(min(args.cpu_rows, N))
+    g = torch.Generator().manual_seed(2026)
+    tdt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[args.dtype]
+    q, k, v, do = (torch.randn((B, H, N, D), generator=g).to(tdt) for _ in range(4))
+    part, micro = O.reference_routing(N, D, args.dtype, training=True, is_causal=causal)
+    t0 = time.perf_counter()
+    ro, rm, rz = T.forward(q, k, v, is_causal=causal, part_len=part, micro=micro, dtype=args.dtype, rows=rows)
+    full_o = torch.zeros((B, H, N, D))
+    full_o[:, :, rows] = ro
+    full_m = torch.full((B * H, N), float("-inf"))
+    full_z = torch.zeros((B * H, N))
+    full_m[:, rows] = rm
+    full_z[:, rows] = rz
+    T.backward(q, k, v, full_o, do, full_m, full_z, is_causal=causal, dtype=args.dtype, rows=rows)
+    ns_secs = time.perf_counter() - t0
+    frac = len(rows) / N if not causal else float((rows + 1).sum()) / (N * (N + 1) / 2)
+    ns_flops = 3.5 * _flops_fwd(B, H, N, D, causal) * frac
+    out["north_star_sample"] = {
+        "value": round(ns_flops / ns_secs / 1e12, 5), "unit": "TFLOP/s", "seconds": round(ns_secs, 3),
+        "sample": f"fwd + bwd at the reference's rounding points (oracle/torch_scan.py, {part}-key partitions) for "
+                  f"query rows 0..{len(rows) - 1} of B{B} H{H} N{N} d{D} {args.dtype} against all keys, one run"}
+    return out
 
 
 if __name__ == "__main__":

@@ -26,7 +26,11 @@ What this restates (paths relative to the reference's
 * ``backward``: ``attention_bwd.py:188-224`` (D, LSE2), ``:309-412`` (dq) and
   ``:415-527`` (dk/dv), including the casts at ``:404``, ``:512``, ``:514``.
 * ``row_stats``: ``attention_bwd.py:227-306``.
-* ``dbias``: ``attention_bwd.py:529-624`` and ``:973-1000``.
+* ``dbias``: ``attention_bwd.py:529-624`` and ``:973-1000`` (``mode="ref"``: the
+  kernel's float32 arithmetic; default float64).
+* ``reference_routing``: the reference's partition and micro-tile widths per call
+  (``attention.py:175-226``, ``attention_bwd.py:130-158``,
+  ``attention_parallel_scan.py:467-468``).
 
 Rounding modes (``mode``):
 
@@ -39,12 +43,18 @@ Rounding modes (``mode``):
   go through the generic kernel (fp32 ``p @ v``, bf16 summaries); fp32 inputs
   stay in fp32 throughout.
 
-Parity pins (``tests/test_oracle.py``): the fp64 mode against the independent
-closed forms below; the ``ref`` mode against the closed forms within the error
-magnitudes the reference publishes (README.md:31, 78-79); monoid identity,
-associativity, partition-count and merge-order invariance; finite differences
-of the closed-form forward for the backward; and the committed fixtures under
-``tests/golden/``.  No part of this module is "parity unpinned".
+Parity pins: the fp64 mode against the independent closed forms below and against
+PyTorch's math SDPA with autograd in float64 (``tests/test_oracle.py``,
+``tests/test_golden.py``); the ``ref`` mode from above, within the error magnitudes the
+reference publishes (README.md:31, 78-79), and from below, by an independent hand fold
+whose fp16 roundings of q, p, s and the output the oracle must reproduce, where deleting
+any one of them fails (``tests/test_oracle_rounding.py``); monoid identity,
+associativity, partition-count and merge-order invariance; finite differences of the
+closed-form forward for the backward; the float32 dbias against the float64 one; the
+routing table against the reference's values; and the committed fixtures under
+``tests/golden/``.  ``oracle/torch_scan.py`` restates the same algorithm with torch CPU
+operations for large shapes and is pinned against this module
+(``tests/test_oracle_torch.py``).  No part of this module is "parity unpinned".
 """
 from __future__ import annotations
 
@@ -486,14 +496,19 @@ def backward(q, k, v, out, dout, row_m, row_z, *, bias=None, is_causal=False, dt
     return dq.reshape(b, h, r, d), dk.reshape(b, h, n, d), dv.reshape(b, h, n, d)
 
 
-def dbias(q, k, v, out, dout, row_m, row_z, *, bias, is_causal=False):
-    """dbias = sum over broadcast dims of ``p*(dp - D)``, fp64.
+def dbias(q, k, v, out, dout, row_m, row_z, *, bias, is_causal=False, mode="fp64"):
+    """dbias = sum over broadcast dims of ``p*(dp - D)``.
 
-    Follows attention_bwd.py:529-624 (kernel: ``p = exp2(s - m)/max(z,1e-30)``) and the
-    broadcast reduction of the dense fallback :987-999.
+    Follows the reference's dense-bias kernel (attention_bwd.py:529-624):
+    ``p = exp2((q.k * scale + bias) * log2e - m) * (1 / max(z, 1e-30))``,
+    ``dp = dO . v``, ``D = rowsum(out * dO)``, and the broadcast reduction of the dense
+    fallback (:987-999).  ``mode="fp64"`` evaluates it in float64; ``mode="ref"`` in float32
+    as the kernel does (fp32 dots, fp32 accumulation over the broadcast pairs).
     """
     b, h, n, d = q.shape
     bh = b * h
+    if mode == "ref":
+        return _dbias_ref32(q, k, v, out, dout, row_m, row_z, bias, is_causal)
     scale = 1.0 / math.sqrt(d)
     qf = np.asarray(q, np.float64).reshape(bh, n, d)
     kf = np.asarray(k, np.float64).reshape(bh, n, d)
@@ -503,6 +518,37 @@ def dbias(q, k, v, out, dout, row_m, row_z, *, bias, is_causal=False):
     bb = np.asarray(canonical_bias(bias, b, h, n), np.float64).reshape(bh, n, n)
     sc = np.matmul(qf, np.swapaxes(kf, -1, -2)) * scale + bb
     return _dbias_from_scores(sc, qf, kf, vf, dof, dd, row_m, row_z, b, h, n, np.shape(bias), is_causal, bb)
+
+
+def _dbias_ref32(q, k, v, out, dout, row_m, row_z, bias, is_causal):
+    """The dense-bias kernel's float32 arithmetic (attention_bwd.py:596-614), per (b, h), then
+    the broadcast dims summed in float32 in increasing (b, h) order."""
+    b, h, n, d = q.shape
+    f32 = np.float32
+    qf, kf, vf, dof, of = (np.asarray(x, f32).reshape(b * h, n, d) for x in (q, k, v, dout, out))
+    bb = np.asarray(canonical_bias(bias, b, h, n), f32).reshape(b * h, n, n)
+    rm = np.asarray(row_m, f32).reshape(b * h, n)
+    inv_z = f32(1.0) / np.maximum(np.asarray(row_z, f32).reshape(b * h, n), f32(1e-30))
+    valid = np.tril(np.ones((n, n), bool)) if is_causal else np.ones((n, n), bool)
+    sc = (np.matmul(qf, np.swapaxes(kf, -1, -2)) * f32(1.0 / math.sqrt(d)) + bb) * f32(LOG2E)
+    sc = np.where(valid[None], sc, f32(-np.inf))
+    with np.errstate(invalid="ignore"):
+        p = np.where(valid[None], _exp2(sc - rm[..., None]) * inv_z[..., None], f32(0)).astype(f32)
+    dp = np.matmul(dof, np.swapaxes(vf, -1, -2))
+    dd = (of * dof).sum(-1, dtype=f32)
+    ds = (p * (dp - dd[..., None])).astype(f32).reshape(b, h, n, n)
+    shape = tuple(np.shape(bias))
+    keep_b = len(shape) == 4 and shape[0] != 1
+    keep_h = (len(shape) == 4 and shape[1] != 1) or (len(shape) == 3 and shape[0] != 1)
+    acc = np.zeros((b if keep_b else 1, h if keep_h else 1, n, n), f32)
+    for bi in range(b):
+        for hi in range(h):
+            acc[bi if keep_b else 0, hi if keep_h else 0] += ds[bi, hi]
+    if len(shape) == 2:
+        return acc[0, 0]
+    if len(shape) == 3:
+        return acc[0]
+    return acc
 
 
 def _dbias_from_scores(sc, qf, kf, vf, dof, dd, row_m, row_z, b, h, n, bias_shape, is_causal, bb):

@@ -86,3 +86,20 @@ def test_every_elsa_kernel_name_maps_to_its_bench_kernel():
 def test_algorithmic_flops():
     assert bench._flops_fwd(1, 8, 16384, 64, False) == 4.0 * 8 * 16384 ** 2 * 64
     assert bench._flops_fwd(1, 1, 4, 2, True) == 4.0 * 2 * (4 * 5 / 2)
+
+
+def test_cpu_baseline_times_baseline_config_1():
+    """cpu_baseline is BASELINE config 1 (B1 H8 N1024 d64 fp32 forward, seed 1234) through the
+    pure-PyTorch restatement, checked against math SDPA, with CPU SDPA and a row sample of the
+    benchmarked step beside it."""
+    import types
+
+    args = types.SimpleNamespace(cpu_rows=64, dtype="fp16")
+    res = bench._cpu_baseline(args, 1, 2, 512, 64, False)
+    assert res["kind"] == "port" and res["unit"] == "TFLOP/s" and res["value"] > 0 and res["cores"] >= 1
+    assert "BASELINE config 1" in res["sample"] and "1234" in res["sample"]
+    assert res["max_abs_vs_math_sdpa_fp64"] < 2e-6  # fp32 restatement against the fp64 closed form
+    assert res["cpu_math_sdpa"]["ms"] > 0
+    assert math.isclose(res["gflops"], 4 * 8 * 1024 ** 2 * 64 / (res["ms"] * 1e-3) / 1e9, rel_tol=1e-3)
+    ns = res["north_star_sample"]
+    assert ns["value"] > 0 and "rows 0..63" in ns["sample"]

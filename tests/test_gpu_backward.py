@@ -122,7 +122,7 @@ def test_bias_gradients(dt, bias_shape):
         assert_parity(host(got), exp, ref, tol, name, dt)
     assert bt.grad.shape == bias.shape
     summed = (shape[0] * shape[1]) // int(np.prod(bias_shape[:-2]))  # (b, h) pairs folded into each entry
-    rdb = O.dbias(qf, kf, vf, fo, dof, fm, fz, bias=bias)
+    rdb = O.dbias(qf, kf, vf, fo, dof, fm, fz, bias=bias, mode="ref")
     assert_parity(host(bt.grad), edb, rdb, tol * summed, "dbias", "fp32")
 
 
@@ -136,7 +136,7 @@ def test_dbias_causal_matches_closed_form():
     eo, em, ez = O.exact_forward(q, k, v, bias=bias, is_causal=True)
     edb = O.dbias(q, k, v, eo, do, em, ez, bias=bias, is_causal=True)
     fo, fm, fz = O.forward(q, k, v, bias=bias, is_causal=True, dtype="fp32", mode="ref")
-    rdb = O.dbias(q, k, v, fo, do, fm, fz, bias=bias, is_causal=True)
+    rdb = O.dbias(q, k, v, fo, do, fm, fz, bias=bias, is_causal=True, mode="ref")
     describe(str(assert_parity(host(db), edb, rdb, GRAD_TOL["fp32"], "dbias", "fp32")))
 
 

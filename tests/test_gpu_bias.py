@@ -100,7 +100,7 @@ def test_biased_forward_and_backward_several_partitions(case):
     # (reference-rounded out and state) and from the exact one
     qf, kf, vf, dof = (x.float().numpy() for x in (q, k, v, do))
     bnp = b32.numpy()
-    rdb = O.dbias(qf, kf, vf, _np(ro), dof, _np(rrm), _np(rrz), bias=bnp, is_causal=causal)
+    rdb = O.dbias(qf, kf, vf, _np(ro), dof, _np(rrm), _np(rrz), bias=bnp, is_causal=causal, mode="ref")
     edb = O.dbias(qf, kf, vf, _np(eo), dof, _np(em), _np(ez), bias=bnp, is_causal=causal)
     summed = (shape[0] * shape[1]) // int(np.prod(bshape[:-2]))
     # the gradient comes back in the bias's own dtype: one ulp of it is allowed on top

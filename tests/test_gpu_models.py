@@ -26,12 +26,14 @@ def _models(builder, img, dtype, train=False):
 
 
 @pytest.mark.parametrize("dt,tol", [(torch.float32, 2e-4), (torch.float16, 2e-2)])
-@pytest.mark.parametrize("builder,img", [(vit_tiny_patch16, 224), (swin_tiny_patch4_window7, 224),
-                                         (vit_tiny_patch16, 512)])
-def test_dropin_forward_matches_sdpa(builder, img, dt, tol):
-    describe(f"dropin fwd {builder.__name__} {img} {dt}")
+@pytest.mark.parametrize("builder,img,batch", [(vit_tiny_patch16, 224, 2), (swin_tiny_patch4_window7, 224, 2),
+                                               (vit_tiny_patch16, 512, 2), (vit_tiny_patch16, 1024, 8),
+                                               (swin_tiny_patch4_window7, 384, 8),
+                                               (swin_tiny_patch4_window7, 512, 8)])
+def test_dropin_forward_matches_sdpa(builder, img, batch, dt, tol):
+    describe(f"dropin fwd {builder.__name__} {img} batch {batch} {dt}")
     ref, elsa = _models(builder, img, dt)
-    x = torch.randn(2, 3, img, img, generator=torch.Generator().manual_seed(7)).cuda()
+    x = torch.randn(batch, 3, img, img, generator=torch.Generator().manual_seed(7)).cuda()
     with torch.no_grad():
         want = ref(x)
         got = elsa(x.to(dt)).float()
@@ -58,6 +60,34 @@ def test_dropin_training_gradients_match_sdpa(builder, img):
         worst = max(worst, err)
         assert err <= 2e-3, (n, err)
     describe(f"  worst relative grad error {worst:.3e}")
+
+
+@pytest.mark.parametrize("builder", [vit_tiny_patch16, swin_tiny_patch4_window7])
+def test_dropin_fp16_training_is_as_accurate_as_sdpa_fp16(builder):
+    """fp16 training step at 224 px, batch 8: the gradients of the fp16 model with the ELSA
+    drop-in and of the same fp16 model on SDPA, each against the fp32 SDPA model; ELSA's
+    error may not exceed twice SDPA's (fp16 rounding everywhere else in the network sets both)."""
+    describe(f"dropin fp16 train {builder.__name__} 224")
+    torch.manual_seed(1234)
+    base = builder(224)
+    elsa = copy.deepcopy(base)
+    elsa_amd.patch_timm_attention_train(elsa)
+    ref32 = copy.deepcopy(base).cuda().train()
+    sdpa16 = copy.deepcopy(base).to("cuda", torch.float16).train()
+    elsa16 = elsa.to("cuda", torch.float16).train()
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(8, 3, 224, 224, generator=g).cuda()
+    labels = torch.randint(0, 1000, (8,), generator=g).cuda()
+    for m, xx in ((ref32, x), (sdpa16, x.half()), (elsa16, x.half())):
+        torch.nn.functional.cross_entropy(m(xx).float(), labels).backward()
+    errs = {"sdpa16": 0.0, "elsa16": 0.0}
+    for name, m in (("sdpa16", sdpa16), ("elsa16", elsa16)):
+        for (n, p), (_, q) in zip(ref32.named_parameters(), m.named_parameters()):
+            assert q.grad is not None and torch.isfinite(q.grad).all(), n
+            rel = (p.grad - q.grad.float()).norm().item() / max(1e-12, p.grad.norm().item())
+            errs[name] = max(errs[name], rel)
+    describe(f"  worst relative grad error (norm) {errs}")
+    assert errs["elsa16"] <= max(2.0 * errs["sdpa16"], 1e-2)
 
 
 @pytest.mark.parametrize("dt,tol", [(torch.float32, 5e-3), (torch.float16, 8e-2)])

@@ -94,13 +94,47 @@ def test_model_pairs_share_weights():
     base, elsa = elsa_amd.make_model_pair(dim=96, depth=2, heads=3)
     for (n1, p1), (n2, p2) in zip(base.state_dict().items(), elsa.state_dict().items()):
         assert n1 == n2 and torch.equal(p1, p2)
-    assert base.blocks[0].attn.backend == "sdpa" and elsa.blocks[0].attn.backend == "elsa"
-    tb, te = elsa_amd.make_train_model_pair(dim=96, depth=1, heads=3)
-    assert isinstance(te, elsa_amd.TrainableTransformerEncoder)
+    assert all(layer.core.backend == "sdpa" for layer in base.layers)
+    assert all(layer.core.backend == "elsa" for layer in elsa.layers)
+    assert base.layers[0].qkv.weight.data_ptr() != elsa.layers[0].qkv.weight.data_ptr()  # copies, not aliases
+    tb, te = elsa_amd.make_train_model_pair(dim=96, depth=1, heads=3, is_causal=True)
+    assert isinstance(te, elsa_amd.TrainableTransformerEncoder) and te.layers[0].core.trainable
+    assert te.layers[0].core.is_causal and te.layers[0].core.elsa_kwargs["algorithm"] == "paper_scan"
     x = torch.randn(1, 16, 96)
     assert base(x).shape == (1, 16, 96) and tb(x).shape == (1, 16, 96)
     with pytest.raises(ValueError, match="divisible"):
         elsa_amd.make_model_pair(dim=95, heads=3)
+    with pytest.raises(ValueError, match="backend"):
+        elsa_amd.TransformerEncoder(dim=96, heads=3, backend="flash")
+    with pytest.raises(ValueError, match="SDPA kind"):
+        elsa_amd.TransformerEncoder(dim=96, heads=3, backend="sdpa", sdpa_kind="fast")
+
+
+def test_encoder_layer_is_the_pre_norm_block():
+    """The SDPA baseline against the same block written out with plain torch ops."""
+    torch.manual_seed(4)
+    base, _ = elsa_amd.make_model_pair(dim=48, depth=2, heads=3, mlp_ratio=2.0, is_causal=True)
+    x = torch.randn(2, 10, 48)
+    want = x
+    for layer in base.layers:
+        h = torch.nn.functional.layer_norm(want, (48,), layer.norm1.weight, layer.norm1.bias)
+        qkv = h @ layer.qkv.weight.T + layer.qkv.bias
+        q, k, v = (t.reshape(2, 10, 3, 16).transpose(1, 2) for t in qkv.split(48, dim=-1))
+        s = (q @ k.transpose(-1, -2)) / 4.0 + torch.triu(torch.full((10, 10), float("-inf")), 1)
+        a = (torch.softmax(s, -1) @ v).transpose(1, 2).reshape(2, 10, 48)
+        want = want + a @ layer.proj.weight.T + layer.proj.bias
+        h = torch.nn.functional.layer_norm(want, (48,), layer.norm2.weight, layer.norm2.bias)
+        h = torch.nn.functional.gelu(h @ layer.fc1.weight.T + layer.fc1.bias)
+        want = want + h @ layer.fc2.weight.T + layer.fc2.bias
+    want = torch.nn.functional.layer_norm(want, (48,), base.norm.weight, base.norm.bias)
+    torch.testing.assert_close(base(x), want, atol=1e-5, rtol=1e-5)
+
+
+def test_inference_encoder_refuses_gradients_through_elsa():
+    _, elsa = elsa_amd.make_model_pair(dim=48, depth=1, heads=3)
+    qkv = torch.zeros(1, 4, 3, 3, 16, requires_grad=True)
+    with pytest.raises(RuntimeError, match="inference-only"):
+        elsa.layers[0].core(qkv)
 
 
 def test_swin_bias_values_and_padded_row_layout():

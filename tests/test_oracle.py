@@ -255,3 +255,20 @@ def test_canonical_bias_errors():
         O.canonical_bias(np.zeros((2, 3, 3)), 1, 3, 3)
     with pytest.raises(ValueError, match="4D bias"):
         O.canonical_bias(np.zeros((2, 2, 3, 3)), 3, 2, 3)
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 9, 9), (1, 3, 9, 9), (2, 1, 9, 9), (3, 9, 9), (9, 9)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_dbias_ref_mode_is_the_fp32_evaluation(shape, causal):
+    """dbias in the reference kernel's float32 arithmetic (attention_bwd.py:596-614) is the float64
+    form up to float32 rounding, on every broadcast rank; its float32 evaluation shows (it is not
+    the float64 value rounded once)."""
+    q, k, v, do = O.make_inputs((2, 3, 9, 8), seed=40, with_dout=True)
+    bias = (np.random.default_rng(40).standard_normal(shape) * 0.3).astype(np.float32)
+    out, rm, rz = O.exact_forward(q, k, v, bias=bias, is_causal=causal)
+    exact = O.dbias(q, k, v, out, do, rm, rz, bias=bias, is_causal=causal)
+    ref = O.dbias(q, k, v, out, do, rm, rz, bias=bias, is_causal=causal, mode="ref")
+    assert ref.dtype == np.float32 and ref.shape == exact.shape
+    err = np.abs(ref - exact).max()
+    assert err <= 2e-6 * max(1.0, np.abs(exact).max()), err
+    assert err > np.abs(exact.astype(np.float32) - exact).max()
