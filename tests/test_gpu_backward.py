@@ -444,4 +444,7 @@ def test_bwd_dbias_matches_bwd_then_dbias(dt, shape, bias_shape, causal):
     x, y = host(db1), host(db2)
     assert np.isfinite(x).all()
     pairs = (b * h) // (bias_b * bias_h)
-    assert np.abs(x - y).max() <= 1e-6 * max(1.0, np.abs(y).max()) * pairs ** 0.5 + 1e-7
+    # two fp32 evaluations of dS: the dk/dv kernel's dP runs over the head dim in one MFMA
+    # chain of D/2 steps, the dbias kernel's in four; their rounding grows with sqrt(D / 32)
+    chain = max(1.0, d / 32) ** 0.5
+    assert np.abs(x - y).max() <= 1e-6 * max(1.0, np.abs(y).max()) * pairs ** 0.5 * chain + 1e-7

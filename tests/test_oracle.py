@@ -272,3 +272,27 @@ def test_dbias_ref_mode_is_the_fp32_evaluation(shape, causal):
     err = np.abs(ref - exact).max()
     assert err <= 2e-6 * max(1.0, np.abs(exact).max()), err
     assert err > np.abs(exact.astype(np.float32) - exact).max()
+
+
+def test_tf32x3_dot_drops_only_the_tail_product():
+    """matmul_tf32x3 against its definition on single products: exact when one operand is a TF32
+    value (its tail is zero), and off by exactly the dropped tail*tail term otherwise; its error
+    on a random dot sits near 2^-22 relative, between TF32 (2^-11) and fp32 (2^-24)."""
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((5, 7)).astype(np.float32)
+    b = rng.standard_normal((7, 4)).astype(np.float32)
+    np.testing.assert_array_equal(O.matmul_tf32x3(O.round_tf32(a), O.round_tf32(b)),
+                                  (O.round_tf32(a).astype(np.float64) @ O.round_tf32(b).astype(np.float64))
+                                  .astype(np.float32))
+    x = np.float32(1.0 + 2 ** -12 + 2 ** -20)  # head 1, tail 2^-12 + 2^-20 (both TF32-exact)
+    hx = O.round_tf32(np.array([x]))[0]
+    assert hx == np.float32(1.0)
+    got = O.matmul_tf32x3(np.array([[x]]), np.array([[x]]))[0, 0]
+    tail = float(x) - 1.0
+    assert got == np.float32(float(x) * float(x) - tail * tail)
+    assert O.round_tf32(np.array([1.0 + 2 ** -11], np.float32))[0] == np.float32(1.0 + 2 ** -10)  # ties away
+    big_a = rng.standard_normal((64, 256)).astype(np.float32)
+    big_b = rng.standard_normal((256, 64)).astype(np.float32)
+    exact = big_a.astype(np.float64) @ big_b.astype(np.float64)
+    rel = np.abs(O.matmul_tf32x3(big_a, big_b) - exact).max() / np.abs(exact).max()
+    assert 2 ** -26 < rel < 2 ** -19, rel
