@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "elsa_struct_size",
     "elsa_fwd_plan_get",
     "elsa_fwd",
+    "elsa_fwd_noalloc",
     "elsa_phase1",
     "elsa_phase2",
     "elsa_bwd_workspace_bytes",
@@ -163,6 +164,7 @@ def load() -> ctypes.CDLL:
     lib.elsa_struct_size.argtypes = [c_int32]
     lib.elsa_fwd_plan_get.argtypes = [ctypes.POINTER(FwdArgs), ctypes.POINTER(FwdPlan)]
     lib.elsa_fwd.argtypes = [ctypes.POINTER(FwdArgs), c_void_p]
+    lib.elsa_fwd_noalloc.argtypes = [ctypes.POINTER(FwdArgs), c_void_p]
     lib.elsa_phase1.argtypes = [ctypes.POINTER(FwdArgs), c_int32, c_int32, c_void_p]
     lib.elsa_phase2.argtypes = [ctypes.POINTER(FwdArgs), c_int32, c_int32, c_void_p]
     lib.elsa_bwd_workspace_bytes.restype = c_size_t
@@ -178,7 +180,7 @@ def load() -> ctypes.CDLL:
     lib.elsa_bwd_dbias.argtypes = [ctypes.POINTER(BwdArgs), c_void_p, c_int32, c_int32, c_void_p]
     lib.elsa_debug_mfma.argtypes = [c_int32, c_void_p, c_void_p, c_void_p, c_void_p]
     lib.elsa_debug_mfma_rate.argtypes = [c_int32, c_void_p, c_void_p, c_int32, c_int32, c_void_p]
-    for fn in ("elsa_fwd_plan_get", "elsa_fwd", "elsa_phase1", "elsa_phase2", "elsa_bwd", "elsa_bwd_stage", "elsa_row_stats",
+    for fn in ("elsa_fwd_plan_get", "elsa_fwd", "elsa_fwd_noalloc", "elsa_phase1", "elsa_phase2", "elsa_bwd", "elsa_bwd_stage", "elsa_row_stats",
                "elsa_dbias", "elsa_bwd_dbias", "elsa_debug_mfma", "elsa_debug_mfma_rate"):
         getattr(lib, fn).restype = c_int32
     if lib.elsa_abi_version() != ABI_VERSION:

@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "elsa_hip.h"
@@ -56,6 +57,12 @@ int check_bias(const elsa_bias_desc& b) {
 
 elsa::BiasView bias_view(const elsa_bias_desc& b) {
   return elsa::BiasView{b.ptr, b.dtype, b.stride_b, b.stride_h, b.stride_q, b.stride_k};
+}
+
+// Phase-1 summaries of P partitions x bh heads x q_chunk rows: m and z (fp32), s (summary dtype)
+size_t fwd_workspace_bytes(int64_t parts, int64_t bh, int64_t q_chunk, int64_t d, int sdt) {
+  const size_t rows = (size_t)parts * bh * q_chunk;
+  return 2 * align256(rows * 4) + align256(rows * d * dtype_size(sdt));
 }
 
 // Partition routing for 256 CUs: at least ~2048 Phase-1 workgroups when the
@@ -119,14 +126,13 @@ int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
     const size_t per_row = (size_t)parts * bh * row_bytes;
     if (per_row * q_chunk > cap) q_chunk = std::max<int64_t>(bm, (int64_t)(cap / per_row) / bm * bm);
   }
-  const size_t rows = (size_t)parts * bh * q_chunk;
   pl->partitions = (int32_t)parts;
   pl->partition_len = (int32_t)part;
   pl->q_chunk = (int32_t)q_chunk;
   pl->block_m = bm;
   pl->key_tile = kt;
   pl->_pad = 0;
-  pl->workspace_bytes = 2 * align256(rows * 4) + align256(rows * d * dtype_size(a->summary_dtype));
+  pl->workspace_bytes = fwd_workspace_bytes(parts, bh, q_chunk, d, a->summary_dtype);
   return ELSA_OK;
 }
 
@@ -261,11 +267,13 @@ int check_layout(const char* name, const void* ptr, const elsa_layout& l, const 
   return ELSA_OK;
 }
 
-int check_fwd_call(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
+// A forward call's plan and operands; the caller's workspace too unless own_workspace is false
+// (elsa_fwd_noalloc brings its own).
+int check_fwd_operands(const elsa_fwd_args* a, elsa_fwd_plan* pl, bool own_workspace) {
   int rc = plan_fwd(a, pl);
   if (rc) return rc;
   if (!a->out) return fail(ELSA_ERR_INVALID, "out must be a non-null device pointer");
-  if (!a->workspace || a->workspace_bytes < pl->workspace_bytes)
+  if (own_workspace && (!a->workspace || a->workspace_bytes < pl->workspace_bytes))
     return fail(ELSA_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", a->workspace_bytes,
                 pl->workspace_bytes);
   if ((rc = check_layout("q", a->q, a->q_layout, a, pl->partition_len, false)) ||
@@ -273,6 +281,24 @@ int check_fwd_call(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
       (rc = check_layout("v", a->v, a->v_layout, a, pl->partition_len, false)) ||
       (rc = check_layout("out", a->out, a->out_layout, a, pl->partition_len, true)))
     return rc;
+  return ELSA_OK;
+}
+
+int check_fwd_call(const elsa_fwd_args* a, elsa_fwd_plan* pl) { return check_fwd_operands(a, pl, true); }
+
+// The forward's q-chunk loop: Phase 1 then Phase 2 per chunk, or the single-partition fold
+// with the finalize in its epilogue.
+int run_fwd(const elsa_fwd_args* a, const elsa_fwd_plan& pl, hipStream_t st) {
+  int rc;
+  for (int q0 = 0; q0 < a->seq_len; q0 += pl.q_chunk) {
+    const int len = std::min(pl.q_chunk, a->seq_len - q0);
+    if (pl.partitions == 1) {
+      if ((rc = run_phase(a, pl, q0, len, st, 3))) return rc;
+      continue;
+    }
+    if ((rc = run_phase(a, pl, q0, len, st, 1))) return rc;
+    if ((rc = run_phase(a, pl, q0, len, st, 2))) return rc;
+  }
   return ELSA_OK;
 }
 
@@ -359,6 +385,73 @@ elsa::BwdParams bwd_params(const elsa_bwd_args* a) {
 
 }  // namespace
 
+// ------------------------------------------------------------------ allocation-free forward
+// Workspace of elsa_fwd_noalloc: the Phase-1 summaries in a file-scope device array, one copy
+// per GPU, held from the library's load until the process ends.  64 MiB takes the north
+// star's summaries (B1 H8 N16384 d64 fp16, two partitions: 35.7 MB) in one q-chunk; larger
+// calls run in several q-chunks over it.  Every call on one GPU uses the same array, so calls
+// that overlap on one GPU (concurrent streams, threads) race on it.
+namespace elsa {
+constexpr size_t kScratchBytes = size_t(64) << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+}  // namespace elsa
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of this GPU's scratch.  Host code never passes the array's own name (a
+// host-side stand-in, not a device address): hipGetSymbolAddress resolves it once per device,
+// with that device current, and the address is kept.
+int scratch_for_stream(void* stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (stream != nullptr) {
+    int sdev = -1;
+    if ((e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev)) != hipSuccess)
+      return hip_fail(e, "hipStreamGetDevice");
+    if (sdev != dev)
+      return fail(ELSA_ERR_INVALID, "elsa_fwd_noalloc: the stream belongs to device %d, the current device is %d",
+                  sdev, dev);
+  }
+  if (dev < 0 || dev >= kMaxDevices) return fail(ELSA_ERR_UNSUPPORTED, "device index %d >= %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(elsa::scratch))) != hipSuccess)
+      return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ELSA_OK;
+}
+
+// elsa_fwd's plan with its q-chunk shortened until the summaries fit the scratch (the same
+// partitions, so every row gets the same fold and merge as from elsa_fwd, bit for bit).
+int fit_plan_to_scratch(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
+  if (pl->workspace_bytes <= elsa::kScratchBytes) return ELSA_OK;
+  const int64_t bh = (int64_t)a->batch * a->heads;
+  const size_t per_row = (size_t)pl->partitions * bh * (8 + (size_t)a->head_dim * dtype_size(a->summary_dtype));
+  int64_t rows = (int64_t)((elsa::kScratchBytes - 3 * 256) / per_row);
+  if (rows >= pl->block_m) rows = rows / pl->block_m * pl->block_m;
+  if (rows < 1)
+    return fail(ELSA_ERR_WORKSPACE,
+                "elsa_fwd_noalloc: one query row needs %zu bytes of Phase-1 summaries (%d partitions x %lld heads), "
+                "beyond the %zu-byte built-in scratch; use elsa_fwd with a workspace",
+                per_row, pl->partitions, (long long)bh, elsa::kScratchBytes);
+  pl->q_chunk = (int32_t)std::min<int64_t>(rows, pl->q_chunk);
+  pl->workspace_bytes = fwd_workspace_bytes(pl->partitions, bh, pl->q_chunk, a->head_dim, a->summary_dtype);
+  if (pl->workspace_bytes > elsa::kScratchBytes)
+    return fail(ELSA_ERR_WORKSPACE, "elsa_fwd_noalloc: %zu bytes of summaries do not fit the scratch",
+                pl->workspace_bytes);
+  return ELSA_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int elsa_abi_version(void) { return ELSA_ABI_VERSION; }
@@ -382,17 +475,20 @@ int elsa_fwd(const elsa_fwd_args* a, void* stream) {
   elsa_fwd_plan pl;
   int rc = check_fwd_call(a, &pl);
   if (rc) return rc;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  for (int q0 = 0; q0 < a->seq_len; q0 += pl.q_chunk) {
-    const int len = std::min(pl.q_chunk, a->seq_len - q0);
-    if (pl.partitions == 1) {
-      if ((rc = run_phase(a, pl, q0, len, st, 3))) return rc;
-      continue;
-    }
-    if ((rc = run_phase(a, pl, q0, len, st, 1))) return rc;
-    if ((rc = run_phase(a, pl, q0, len, st, 2))) return rc;
-  }
-  return ELSA_OK;
+  return run_fwd(a, pl, static_cast<hipStream_t>(stream));
+}
+
+int elsa_fwd_noalloc(const elsa_fwd_args* args, void* stream) {
+  elsa_fwd_plan pl;
+  int rc = check_fwd_operands(args, &pl, false);
+  if (rc) return rc;
+  if ((rc = fit_plan_to_scratch(args, &pl))) return rc;
+  void* ws = nullptr;
+  if ((rc = scratch_for_stream(stream, &ws))) return rc;
+  elsa_fwd_args a = *args;  // the same call with the scratch as its workspace
+  a.workspace = ws;
+  a.workspace_bytes = elsa::kScratchBytes;
+  return run_fwd(&a, pl, static_cast<hipStream_t>(stream));
 }
 
 int elsa_phase1(const elsa_fwd_args* a, int32_t q_start, int32_t q_len, void* stream) {

@@ -145,6 +145,16 @@ size_t elsa_struct_size(int which); /* 0 fwd_args, 1 fwd_plan, 2 bwd_args, 3 bia
 int elsa_fwd_plan_get(const elsa_fwd_args* args, elsa_fwd_plan* plan);
 /* Full forward: for each q-chunk, Phase 1 (summaries -> workspace) then Phase 2. */
 int elsa_fwd(const elsa_fwd_args* args, void* stream);
+/* elsa_fwd without a caller workspace: the Phase-1 summaries go to a 64 MiB device array built
+ * into the library (one per GPU, held until the process ends), so the call allocates nothing.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops).  args->workspace and workspace_bytes
+ * are ignored; out and the row state are written exactly as elsa_fwd writes them (the same
+ * partitions, q-chunked to fit the array).  A call whose single query row needs more than
+ * 64 MiB of summaries (partitions x B*H x (8 + head_dim * summary bytes)) returns
+ * ELSA_ERR_WORKSPACE.  `stream` must belong to the current device.  All calls on one GPU share
+ * its array: calls that overlap on one GPU race. */
+int elsa_fwd_noalloc(const elsa_fwd_args* args, void* stream);
 /* The two passes separately, for rows [q_start, q_start+q_len) (q_len <= plan.q_chunk). */
 int elsa_phase1(const elsa_fwd_args* args, int32_t q_start, int32_t q_len, void* stream);
 int elsa_phase2(const elsa_fwd_args* args, int32_t q_start, int32_t q_len, void* stream);

@@ -153,6 +153,32 @@ def test_fwd_rejects_missing_workspace_without_launching():
     assert lib.elsa_fwd(ctypes.byref(a), None) == _lib.ELSA_ERR_INVALID
 
 
+def test_fwd_noalloc_rejects_rows_beyond_its_scratch_without_launching():
+    """elsa_fwd_noalloc (summaries in the library's 64 MiB device array) refuses a call of which
+    a single query row needs more than the array, before any HIP call."""
+    lib = _lib.load()
+    a = _args(n=8192, bh=(64, 64), part=64)  # 128 partitions x 4096 heads x 136 B = 71 MB per row
+    a.q = a.k = a.v = a.out = 1 << 12
+    rc = lib.elsa_fwd_noalloc(ctypes.byref(a), None)
+    assert rc == _lib.ELSA_ERR_WORKSPACE
+    msg = lib.elsa_last_error().decode()
+    assert "elsa_fwd_noalloc" in msg and "scratch" in msg
+    a.q = None
+    assert lib.elsa_fwd_noalloc(ctypes.byref(a), None) == _lib.ELSA_ERR_INVALID
+
+
+def test_library_imports_no_device_allocation():
+    """No entry point of libelsa_hip.so can allocate or free device memory: the library does not
+    import any HIP allocation or release routine (callers bring every buffer, elsa_fwd_noalloc
+    uses the library's own device array)."""
+    import subprocess
+
+    syms = subprocess.run(["nm", "-D", "--undefined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                          check=True).stdout
+    hip = sorted({line.split()[-1].split("@")[0] for line in syms.splitlines() if "hip" in line})
+    assert hip and not [s for s in hip if re.search(r"(?i)alloc|free|mempool|hostregister", s)], hip
+
+
 def test_bwd_and_dbias_reject_bad_args_without_launching():
     lib = _lib.load()
     b = _lib.BwdArgs()
