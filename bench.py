@@ -74,7 +74,7 @@ def _args():
 
 
 # rocprofv3 kernel-name fragment -> bench kernel name
-_KERNEL_KEYS = (("phase1_half_kernel", "phase1_fold"), ("phase1_kernel", "phase1_fold"),
+_KERNEL_KEYS = (("phase1_half_kernel", "phase1_fold"), ("phase1_pp_kernel", "phase1_fold"), ("phase1_kernel", "phase1_fold"),
                 ("phase2_kernel", "phase2_merge"), ("phase2_np_kernel", "phase2_merge"),
                 ("bwd_pre_kernel", "bwd_preprocess"),
                 ("bwd_dq_half_kernel", "bwd_dq"), ("bwd_dq_kernel", "bwd_dq"),
