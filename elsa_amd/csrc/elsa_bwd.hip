@@ -532,9 +532,9 @@ void bwd_dq_half_kernel(const BwdParams p) {
   }
   const int k_end = p.causal ? wg_last + 1 : p.N;
   // -D of this lane's row: the dP^T product starts from it and yields dP - D directly.  The
-  // 16 registers of that constant would spill in the bias and D = 128 variants, which
-  // subtract D from each score instead.
-  constexpr bool SEED_D = !HAS_BIAS && DP <= 64;
+  // 16 registers per row tile of that constant would spill in the bias, D = 128 and two-tile
+  // variants, which subtract D from each score instead.
+  constexpr bool SEED_D = !HAS_BIAS && DP <= 64 && RT == 1;
   f32x16 ndd[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
@@ -543,14 +543,9 @@ void bwd_dq_half_kernel(const BwdParams p) {
 
   // element offsets of this thread's staging chunks inside a stage (row strides are
   // below 2^25 elements, checked by the API, so 64 rows fit in 32 bits)
-  int32_t koff[NCH], voff[NCH];
-  static_for<0, NCH>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    const int ci = tid + i * NT;
-    const int r = ci / CPR, d0 = (ci % CPR) * 8;
-    koff[i] = r * (int32_t)p.ks[2] + d0;
-    voff[i] = r * (int32_t)p.vs[2] + d0;
-  });
+  // (chunk tid + NT i sits NT / CPR rows below chunk tid)
+  const int32_t koff0 = (tid / CPR) * (int32_t)p.ks[2] + (tid % CPR) * 8;
+  const int32_t voff0 = (tid / CPR) * (int32_t)p.vs[2] + (tid % CPR) * 8;
   // staging registers: set S holds one 64-key stage on its way from global memory to LDS
   Chunk16 kreg[2][NCH], vreg[2][NCH];
   auto gload = [&](int t0, auto SET) {
@@ -562,8 +557,8 @@ static_for<0, NCH>([&](auto I) {
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
       if (t0 + r < k_end && d0 < p.D) {
-        kreg[S][i] = *reinterpret_cast<const Chunk16*>(kt + koff[i]);
-        vreg[S][i] = *reinterpret_cast<const Chunk16*>(vt + voff[i]);
+        kreg[S][i] = *reinterpret_cast<const Chunk16*>(kt + koff0 + (int64_t)(i * (NT / CPR)) * p.ks[2]);
+        vreg[S][i] = *reinterpret_cast<const Chunk16*>(vt + voff0 + (int64_t)(i * (NT / CPR)) * p.vs[2]);
       } else {
         kreg[S][i] = Chunk16{};
         vreg[S][i] = Chunk16{};
@@ -603,9 +598,10 @@ static_for<0, NCH>([&](auto I) {
           kf[kk] = *reinterpret_cast<const F*>(krow + kk * 16);
           vf[kk] = *reinterpret_cast<const F*>(vrow + kk * 16);
         }
-        f32x16 ds[RT];
+        F dsp[RT][2];  // dS of the sub-tile, rounded to T: the B operand of the dQ^T product
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
+          f32x16 ds;
           f32x16 s = M::mma(kf[0], qf[rt][0], f32x16{}), dp = M::mma(vf[0], gf[rt][0], ndd[rt]);
 #pragma unroll
           for (int kk = 1; kk < NKK; ++kk) {
@@ -622,22 +618,26 @@ static_for<0, NCH>([&](auto I) {
               const bool ok = live[rt] && key < k_end && (!p.causal || key <= my_row);
               const float x = fmaf(s[r], p.scale_log2, nl);
               const float pr = ok ? fast_exp2(fmaf(load_bias_b(p.bias, bi, hi, my_row, key), kLog2e, x)) : 0.f;
-              ds[rt][r] = pr * (dp[r] - dd[rt]);
+              ds[r] = pr * (dp[r] - dd[rt]);
             }
           } else {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) ds[rt][r] = fast_exp2(fmaf(s[r], p.scale_log2, nl));
+            for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], p.scale_log2, nl));
             if (!full) {
               asm volatile("");  // keep this a branch: boundary tiles only
 #pragma unroll
               for (int r = 0; r < 16; ++r) {
                 const int key = t0 + sub * 32 + key_of_reg(r, g);
-                if (!(key < k_end && (!p.causal || key <= my_row))) ds[rt][r] = 0.f;
+                if (!(key < k_end && (!p.causal || key <= my_row))) ds[r] = 0.f;
               }
             }
 #pragma unroll
-            for (int r = 0; r < 16; ++r) ds[rt][r] *= SEED_D ? dp[r] : dp[r] - dd[rt];
+            for (int r = 0; r < 16; ++r) ds[r] *= SEED_D ? dp[r] : dp[r] - dd[rt];
           }
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int t = 0; t < 8; ++t) dsp[rt][j][t] = static_cast<T>(ds[j * 8 + t]);
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -645,23 +645,20 @@ static_for<0, NCH>([&](auto I) {
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) ka[dt] = tr_frag<T>(ks + (sub * 32 + 16 * j + tr_row) * KS, KS, dt * 32 + tr_col);
 #pragma unroll
-          for (int rt = 0; rt < RT; ++rt) {
-            F b;
+          for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int t = 0; t < 8; ++t) b[t] = static_cast<T>(ds[rt][j * 8 + t]);
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) acc[rt][dt] = M::mma(ka[dt], b, acc[rt][dt]);
-          }
+            for (int dt = 0; dt < NDT; ++dt) acc[rt][dt] = M::mma(ka[dt], dsp[rt][j], acc[rt][dt]);
         }
       }
     }
   };
   const auto S0 = std::integral_constant<int, 0>{};
   const auto S1 = std::integral_constant<int, 1>{};
-  if constexpr (DP <= 64) {
+  if constexpr (DP <= 64 && RT == 1) {
     // global loads two stages ahead (as in dK/dV; 16K d64: 0.857 -> 0.842 ms).  At D = 128 the
     // second register set spills at two waves per SIMD, and one wave per SIMD is slower still
-    // (1.64 against 1.87-2.07 ms), so that width keeps one stage of prefetch
+    // (1.64 against 1.87-2.07 ms), so that width keeps one stage of prefetch, and so does the
+    // two-tile variant (255 VGPRs with one set)
     gload(0, S0);
     sstore(0, S0);
     if (ntiles > 1) gload(KT, S1);
@@ -1199,7 +1196,18 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
     constexpr int R = 1;  // one 32-wide tile per wave: 2 waves per SIMD beat wider tiles at 1
     const dim3 grid((p.N + 32 * R * W - 1) / (32 * R * W), p.BH);
     if (stage < 0 || stage == 1) {
-      hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, W, B>), grid, dim3(64 * W), 0, st, p);
+      // dq with two 32-row tiles per wave (256-row work-groups): each K/V fragment read from LDS
+      // feeds both tiles, halving the LDS reads per MFMA.  Non-causal, unbiased, D <= 64, and only
+      // where the grid still puts two work-groups on every CU.  B1 H8 d64 16K: fp16 0.875 -> 0.814
+      // ms, bf16 0.841 -> 0.768 ms; causal 16K 0.479 against 0.510 ms and 4K (128 work-groups)
+      // 0.074 against 0.111 ms stay on the 32-row kernel.
+      const dim3 grid2((p.N + 255) / 256, p.BH);
+      bool wide = false;
+      if constexpr (DP <= 64 && !B) {
+        wide = !p.causal && (int64_t)grid2.x * grid2.y >= 512;
+        if (wide) hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, 2, W, false>), grid2, dim3(64 * W), 0, st, p);
+      }
+      if (!wide) hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, W, B>), grid, dim3(64 * W), 0, st, p);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (stage < 0 || stage == 2) {

@@ -135,6 +135,8 @@ FULL = [
     ((8, 3, 2305, 64), "fp16", False),
     ((1, 8, 2048, 64), "fp16", True),    # causal config: N=2048 forward and backward
     ((1, 8, 4097, 64), "fp16", True),    # causal NEEDS_MASK length
+    ((4, 32, 1024, 64), "fp16", False),  # 512 dq work-groups of 256 rows: the two-tile dq kernel
+    ((2, 64, 1024, 64), "bf16", False),
 ]
 
 
