@@ -693,14 +693,14 @@ void phase1_half_kernel(const Phase1Params p) {
 }
 
 // ------------------------------------------------------------------ Phase 1, ping-pong
-// The prescaled fp16 fold (no bias, no causal mask) with 8 waves of 64 rows per workgroup,
+// The fp16/bf16 fold without bias or causal mask, with 8 waves of 64 rows per workgroup,
 // two per SIMD, in two groups (waves 0-3 and 4-7) that take turns: while one group's waves
 // run the matrix products of a stage, the other group's waves on the same SIMDs run the
 // softmax of theirs.  Workgroup barriers delimit the phases, so the matrix core and the
 // vector ALU of a SIMD each serve one wave at a time instead of both waves queueing for the
 // same unit.  A wave's stage i is
 //   M_i (matrix): P^T V of stage i-1 (packed p kept from V_{i-1}), then S = K Q^T of stage i
-//                 from the reference -m_run (as in phase1_half_kernel);
+//                 (PRE, q prescaled: from the reference -m_run, as in phase1_half_kernel);
 //   V_i (vector): mask, max, lazy raise, p = exp2(S), row sums, packing of p.
 // Phase ph: group 0 runs M_i at ph = 2i and V_i at ph = 2i+1, group 1 one phase later; both
 // run 2n + 2 phases (n key stages), so every wave meets every barrier.
@@ -710,7 +710,7 @@ void phase1_half_kernel(const Phase1Params p) {
 // from ph = 2i+2 on.
 // Measured (per-wave timestamps): the matrix phase takes about three times as long as the
 // vector phase, and the kernel is 5% faster than the two-waves-per-SIMD fold at 16K-64K keys.
-template <typename T, int DP>
+template <typename T, int DP, bool PRE>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void phase1_pp_kernel(const Phase1Params p) {
   using M = Mfma<T>;
@@ -749,10 +749,13 @@ void phase1_pp_kernel(const Phase1Params p) {
     for (int kk = 0; kk < NKK; ++kk) {
       const int d0 = kk * 16 + g * 8;
       qf[rt][kk] = load_frag<T>(Q + (int64_t)(ok ? row : 0) * p.qs[2] + d0, ok && d0 < p.D);
+      if constexpr (PRE) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) qf[rt][kk][t] = static_cast<T>(static_cast<float>(qf[rt][kk][t]) * p.scale_log2);
+        for (int t = 0; t < 8; ++t) qf[rt][kk][t] = static_cast<T>(static_cast<float>(qf[rt][kk][t]) * p.scale_log2);
+      }
     }
   }
+  const float cs = p.scale_log2;
 
   const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
@@ -773,14 +776,15 @@ void phase1_pp_kernel(const Phase1Params p) {
   Chunk16 kreg[NCH], vreg[NCH];
 
   f32x16 oacc[RT][NDT];
-  f32x16 negref[RT];  // -ref in every register: the accumulator input of the stage's QK^T product
+  // PRE: -ref in every register, the accumulator input of the stage's QK^T product
+  f32x16 negref[PRE ? RT : 1];
   float m_run[RT], m_true[RT], z_lane[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     m_run[rt] = kNegInf;
     m_true[rt] = kNegInf;
     z_lane[rt] = 0.f;
-    negref[rt] = f32x16{};
+    if constexpr (PRE) negref[rt] = f32x16{};
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) oacc[rt][dt] = f32x16{};
   }
@@ -842,7 +846,11 @@ void phase1_pp_kernel(const Phase1Params p) {
         for (int kk = 0; kk < NKK; ++kk) kf[kk] = *reinterpret_cast<const F*>(krow + kk * 16);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-          s[rt][sub] = M::mma(kf[0], qf[rt][0], negref[rt]);
+          if constexpr (PRE) {
+            s[rt][sub] = M::mma(kf[0], qf[rt][0], negref[rt]);
+          } else {
+            s[rt][sub] = M::mma(kf[0], qf[rt][0], f32x16{});
+          }
 #pragma unroll
           for (int kk = 1; kk < NKK; ++kk) s[rt][sub] = M::mma(kf[kk], qf[rt][kk], s[rt][sub]);
         }
@@ -874,7 +882,11 @@ void phase1_pp_kernel(const Phase1Params p) {
           mx1 = fmaxf(fmaxf(mx1, s[rt][sub][r + 2]), s[rt][sub][r + 3]);
         }
       mx = wave_max_pair(fmaxf(mx, mx1));
-      m_tile[rt] = mx - negref[rt][0];  // the product started from -ref
+      if constexpr (PRE) {
+        m_tile[rt] = mx - negref[rt][0];  // the product started from -ref
+      } else {
+        m_tile[rt] = mx * cs;
+      }
       m_true[rt] = fmaxf(m_true[rt], m_tile[rt]);
       raise |= m_tile[rt] > m_run[rt] + kLazyTau;
     }
@@ -889,21 +901,24 @@ void phase1_pp_kernel(const Phase1Params p) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) oacc[rt][dt][r] *= alpha;
         m_run[rt] = m_new;
-        // the scores are relative to the old reference: move them to the new one (a row still at
-        // -inf has only -inf scores and keeps reference 0)
-        const float ref = (m_new == kNegInf) ? 0.f : m_new;
-        const float shift = ref + negref[rt][0];
+        if constexpr (PRE) {
+          // the scores are relative to the old reference: move them to the new one (a row still
+          // at -inf has only -inf scores and keeps reference 0)
+          const float ref = (m_new == kNegInf) ? 0.f : m_new;
+          const float shift = ref + negref[rt][0];
 #pragma unroll
-        for (int sub = 0; sub < NSUB; ++sub)
+          for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) s[rt][sub][r] -= shift;
+            for (int r = 0; r < 16; ++r) s[rt][sub][r] -= shift;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) negref[rt][r] = -ref;
+          for (int r = 0; r < 16; ++r) negref[rt][r] = -ref;
+        }
       }
     }
     // the row sums in phase1_half_kernel's order, so that both kernels give the same bits
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
+      const float nm = (m_run[rt] == kNegInf) ? 0.f : -m_run[rt];
       float zs = 0.f;
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub)
@@ -911,7 +926,7 @@ void phase1_pp_kernel(const Phase1Params p) {
         for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int t = 0; t < 8; ++t) {
-            const float pr = fast_exp2(s[rt][sub][j * 8 + t]);
+            const float pr = PRE ? fast_exp2(s[rt][sub][j * 8 + t]) : fast_exp2(fmaf(s[rt][sub][j * 8 + t], cs, nm));
             pk[rt][sub][j][t] = static_cast<T>(pr);
             zs += pr;
           }
@@ -1135,16 +1150,25 @@ template <typename T, int DP, int RT, int W, bool B>
 static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
   constexpr int BM = 32 * RT * W;
   const dim3 grid((p.q_len + BM - 1) / BM, p.BH, p.P);
-  if constexpr (!B && DP == 64 && std::is_same<T, f16>::value) {
+  if constexpr (!B && DP == 64 && RT == 2 && W == 4) {
     // 512-row ping-pong workgroups for partitions of at least 16 key stages (the 2n + 2 phases
     // of n stages pay two phases of fill): B1 H8 fp16 Phase 1 at 16K keys 0.599 -> 0.564 ms,
     // 64K 8.59 -> 8.13 ms, 8K 0.181 -> 0.175 ms; at 4K (256-key partitions) 0.054 against
     // 0.061 ms.  Both kernels give the same bits, so the choice never changes a result.
     const dim3 g2((p.q_len + 511) / 512, p.BH, p.P);
-    if (p.prescale_q && RT == 2 && W == 4 && !p.causal && p.part_len >= 1024) {
-      hipLaunchKernelGGL((phase1_pp_kernel<T, DP>), g2, dim3(512), 0, st, p);
+    if (!p.causal && p.part_len >= 1024) {
+      bool done = false;
+      if constexpr (std::is_same<T, f16>::value) {
+        if (p.prescale_q) {
+          hipLaunchKernelGGL((phase1_pp_kernel<T, DP, true>), g2, dim3(512), 0, st, p);
+          done = true;
+        }
+      }
+      if (!done) hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false>), g2, dim3(512), 0, st, p);
       return hipGetLastError();
     }
+  }
+  if constexpr (!B && DP == 64 && std::is_same<T, f16>::value) {
     if (p.prescale_q) {
       hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, false, true>), grid, dim3(64 * W), 0, st, p);
       return hipGetLastError();
