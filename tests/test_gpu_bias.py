@@ -26,7 +26,7 @@ pytestmark = pytest.mark.gpu
 N = 1025
 PART = 512
 
-# q/k/v dtype, bias dtype, bias layout, causal, bias shape
+# q/k/v dtype, bias dtype, bias layout, causal, bias shape[, q/k/v shape (default B2 H2)]
 CASES = [
     ("fp16", "fp16", "padded", False, (2, N, N)),
     ("fp16", "fp16", "dense", True, (2, N, N)),
@@ -34,11 +34,14 @@ CASES = [
     ("bf16", "bf16", "dense", False, (1, 2, N, N)),
     ("fp16", "bf16", "padded", False, (N, N)),
     ("bf16", "fp16", "dense", True, (2, 1, N, N)),
+    # B4 H32: enough 256-row blocks for the 8-wave dq and dK/dV work-groups
+    ("fp16", "fp16", "padded", True, (32, N, N), (4, 32, N, 64)),
 ]
 
 
 def _ids(c):
-    return f"{c[0]}-bias{c[1]}-{c[2]}-{'causal' if c[3] else 'full'}-{'x'.join(map(str, c[4][:-2])) or 'nn'}"
+    tail = f"-B{c[5][0]}H{c[5][1]}" if len(c) > 5 else ""
+    return f"{c[0]}-bias{c[1]}-{c[2]}-{'causal' if c[3] else 'full'}-{'x'.join(map(str, c[4][:-2])) or 'nn'}{tail}"
 
 
 def _bias_leaf(values: torch.Tensor, layout: str):
@@ -59,9 +62,9 @@ def _np(t):
 
 @pytest.mark.parametrize("case", CASES, ids=[_ids(c) for c in CASES])
 def test_biased_forward_and_backward_several_partitions(case):
-    dt, bdt, layout, causal, bshape = case
+    dt, bdt, layout, causal, bshape = case[:5]
     describe(f"biased fwd+bwd {_ids(case)}")
-    shape = (2, 2, N, 64)
+    shape = case[5] if len(case) > 5 else (2, 2, N, 64)
     g = torch.Generator().manual_seed(600 + len(bshape))
     q, k, v, do = (torch.randn(shape, generator=g).to(TORCH_DT[dt]) for _ in range(4))
     bias = (torch.randn(bshape, generator=g) * 0.5).to(TORCH_DT[bdt])

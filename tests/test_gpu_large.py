@@ -137,6 +137,7 @@ FULL = [
     ((1, 8, 4097, 64), "fp16", True),    # causal NEEDS_MASK length
     ((4, 32, 1024, 64), "fp16", False),  # 512 dq work-groups of 256 rows: the two-tile dq kernel
     ((2, 64, 1024, 64), "bf16", False),
+    ((4, 32, 1024, 64), "fp16", True),   # causal: the 8-wave dq and dK/dV work-groups
 ]
 
 
