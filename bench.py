@@ -1,9 +1,10 @@
 """Benchmark of the ELSA two-pass attention hot path on one MI355X.
 
-One step = the training-path attention of BASELINE config 2 at the north-star shape:
-two-pass forward with row state (Phase 1 fold on MFMA -> HBM summaries -> Phase 2
-merge) plus the exact-recompute backward (preprocess, dq, dk/dv), B=1 H=8 N=16384
-d=64 fp16, non-causal, synthetic N(0,1) q/k/v/dO (seed 2026) resident in HBM.
+One step = the training-path attention of BASELINE config 2 at the north-star shape, through
+twopass_attention_train as the reference's benchmarks/bench_bwd.py times it: two-pass forward
+keeping the row state the backward reads (Phase 1 fold on MFMA -> HBM summaries -> Phase 2
+merge) plus the exact-recompute backward (preprocess, dq, dk/dv), B=1 H=8 N=16384 d=64 fp16,
+non-causal, synthetic N(0,1) q/k/v/dO (seed 2026) resident in HBM.
 
 Prints ONE JSON line.  ``value`` is the algorithmic fwd+bwd throughput
 (3.5 * 4*B*H*N^2*d flop per step, recompute not counted).  ``kernels`` holds each
@@ -208,9 +209,15 @@ def main() -> int:
     print(f"bench: {shape} {args.dtype} causal={causal} steps={args.steps} warmup={args.warmup}", file=sys.stderr,
           flush=True)
 
+    # one training step through the reference's training entry point (its benchmarks/bench_bwd.py
+    # times twopass_attention_train(...).backward(dout)): forward with the row state the backward
+    # reads, then the recompute backward; torch.autograd.grad returns the gradients without
+    # accumulating them into .grad
+    qg, kg, vg = (t.detach().requires_grad_() for t in (q, k, v))
+
     def step():
-        out, rm, rz = elsa_amd.twopass_attention_with_state(q, k, v, is_causal=causal, block_n=args.block_n)
-        return elsa_amd.twopass_attention_backward(q, k, v, out, do, is_causal=causal, row_m=rm, row_z=rz)
+        out = elsa_amd.twopass_attention_train(qg, kg, vg, is_causal=causal, block_n=args.block_n)
+        return torch.autograd.grad(out, (qg, kg, vg), do)
 
     for _ in range(args.warmup):
         step()
@@ -235,7 +242,8 @@ def main() -> int:
     rm = torch.empty((B * H, N), device=dev, dtype=torch.float32)
     rz = torch.empty_like(rm)
     fa = _make_fwd_args(q, k, v, out, rm, rz, _BiasMeta(None, 0, 0, 0, 0, False), is_causal=causal,
-                        summary_dtype=dt, partition_len=args.block_n, q_chunk=None, scale=1.0 / math.sqrt(D))
+                        summary_dtype=dt, partition_len=args.block_n, q_chunk=None, scale=1.0 / math.sqrt(D),
+                        exact_row_max=False)  # the training forward's state, as in the step above
     ws_f = torch.empty(plan["workspace_bytes"], dtype=torch.uint8, device=dev)
     fa.workspace, fa.workspace_bytes = ws_f.data_ptr(), plan["workspace_bytes"]
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
@@ -347,7 +355,7 @@ def main() -> int:
         "dtype": args.dtype,
         "data": ("synthetic: q,k,v,dO ~ N(0,1), torch.Generator seed 2026, resident in HBM" if args.fill == "randn"
                  else f"synthetic, diagnostic fill '{args.fill}' (not the benchmark input)"),
-        "config": {"workload": "ELSA two-pass attention fwd(with row state)+bwd, "
+        "config": {"workload": "ELSA two-pass attention training step (twopass_attention_train fwd + bwd), "
                                + ("causal" if causal else "non-causal"),
                    "batch": B, "heads": H, "seq_len": N, "head_dim": D,
                    "partitions": plan["partitions"], "partition_len": plan["partition_len"],

@@ -94,6 +94,7 @@ class FwdArgs(ctypes.Structure):
         ("k_layout", Layout),
         ("v_layout", Layout),
         ("out_layout", Layout),
+        ("exact_row_max", c_int32),
     ]
 
 
@@ -144,7 +145,7 @@ class BwdArgs(ctypes.Structure):
 
 
 _STRUCTS = {0: FwdArgs, 1: FwdPlan, 2: BwdArgs, 3: BiasDesc, 4: Layout}
-ABI_VERSION = 3
+ABI_VERSION = 4
 _lib: Optional[ctypes.CDLL] = None
 
 

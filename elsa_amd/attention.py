@@ -189,7 +189,7 @@ def _pad_head_dim(x: torch.Tensor) -> torch.Tensor:
 
 
 def _make_fwd_args(q_c, k_c, v_c, out, row_m, row_z, bias_meta: _BiasMeta, *, is_causal, summary_dtype,
-                   partition_len, q_chunk, scale) -> _lib.FwdArgs:
+                   partition_len, q_chunk, scale, exact_row_max=True) -> _lib.FwdArgs:
     batch, heads, seq_len, head_dim = map(int, q_c.shape)
     a = _lib.FwdArgs()
     a.q, a.k, a.v, a.out = q_c.data_ptr(), k_c.data_ptr(), v_c.data_ptr(), out.data_ptr()
@@ -206,6 +206,7 @@ def _make_fwd_args(q_c, k_c, v_c, out, row_m, row_z, bias_meta: _BiasMeta, *, is
     a.scale = float(scale)
     a.q_layout, a.k_layout, a.v_layout = (_lib.layout_of(t) for t in (q_c, k_c, v_c))
     a.out_layout = _lib.layout_of(out)
+    a.exact_row_max = 1 if exact_row_max else 0
     return a
 
 
@@ -221,8 +222,13 @@ def _elsa_forward(
     q_chunk: Optional[int],
     want_state: bool,
     out_bnhd: bool = False,
+    exact_row_max: bool = True,
 ):
     """Run Phase 1 + Phase 2 on the HIP library.  Returns (out, row_m, row_z, q_c, k_c, v_c).
+
+    ``exact_row_max`` False lets row_m be the fold's lazy reference (at most 8 below the row
+    maximum, row_z relative to it): the same log-sum-exp for the backward, and the fp16/bf16 d64
+    fold skips most per-stage maxima.  A forward without state takes that path.
 
     q, k, v may be strided views (read in place when ``_operand`` allows); ``out_bnhd``
     allocates the output as [B, N, H, D] memory (returned as its [B, H, N, D] view), so
@@ -242,7 +248,8 @@ def _elsa_forward(
     row_m = torch.empty((batch * heads, seq_len), device=q.device, dtype=torch.float32) if want_state else None
     row_z = torch.empty_like(row_m) if want_state else None
     args = _make_fwd_args(qp, kp, vp, out, row_m, row_z, bias_meta, is_causal=is_causal,
-                          summary_dtype=summary_dtype, partition_len=partition_len, q_chunk=q_chunk, scale=scale)
+                          summary_dtype=summary_dtype, partition_len=partition_len, q_chunk=q_chunk, scale=scale,
+                          exact_row_max=exact_row_max and want_state)
     plan = _lib.FwdPlan()
     _lib.check(lib.elsa_fwd_plan_get(ctypes.byref(args), ctypes.byref(plan)), "elsa_fwd_plan_get")
     ws = torch.empty(int(plan.workspace_bytes), dtype=torch.uint8, device=q.device)

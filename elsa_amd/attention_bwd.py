@@ -59,8 +59,11 @@ def twopass_attention_with_state(
 
 def _with_state(q, k, v, *, bias=None, is_causal=False, block_m=None, block_n=None, q_chunk_size=None,
                 summary_dtype=None, phase1_warps=None, phase2_warps=None, phase1_stages=None, phase2_stages=None,
-                input_precision="auto", algorithm="auto", return_contiguous_inputs=False, out_bnhd=False):
-    """twopass_attention_with_state; ``out_bnhd`` returns out as a [B,H,N,D] view of [B,N,H,D] memory."""
+                input_precision="auto", algorithm="auto", return_contiguous_inputs=False, out_bnhd=False,
+                exact_row_max=True):
+    """twopass_attention_with_state; ``out_bnhd`` returns out as a [B,H,N,D] view of [B,N,H,D] memory.
+    The training autograd functions pass ``exact_row_max=False``: their row state only feeds the
+    backward, which reads row_m + log2(row_z)."""
     _check_qkv(q, k, v, "twopass_attention_with_state")
     batch, heads, seq_len, head_dim = map(int, q.shape)
     if seq_len > 0:
@@ -77,7 +80,7 @@ def _with_state(q, k, v, *, bias=None, is_causal=False, block_m=None, block_n=No
         return out_empty, empty_state, empty_state
     out, row_m, row_z, q_c, k_c, v_c = _elsa_forward(
         q, k, v, bias=bias, is_causal=is_causal, summary_dtype=sdt, partition_len=part, q_chunk=qc, want_state=True,
-        out_bnhd=out_bnhd,
+        out_bnhd=out_bnhd, exact_row_max=exact_row_max,
     )
     if return_contiguous_inputs:
         return out, row_m, row_z, q_c.contiguous(), k_c.contiguous(), v_c.contiguous()
@@ -284,7 +287,8 @@ class _TwopassAttentionAutograd(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, bias, is_causal, fwd_kwargs, bwd_kwargs, out_bnhd=False):
-        out, row_m, row_z = _with_state(q, k, v, bias=bias, is_causal=is_causal, out_bnhd=out_bnhd, **fwd_kwargs)
+        out, row_m, row_z = _with_state(q, k, v, bias=bias, is_causal=is_causal, out_bnhd=out_bnhd,
+                                        exact_row_max=False, **fwd_kwargs)
         _save(ctx, (q, k, v), out, bias, row_m, row_z, is_causal, bwd_kwargs)
         return out
 
@@ -312,7 +316,8 @@ class _TwopassQkvAutograd(torch.autograd.Function):
     @staticmethod
     def forward(ctx, qkv, bias, is_causal, fwd_kwargs, bwd_kwargs):
         q, k, v = qkv.permute(2, 0, 3, 1, 4).unbind(0)
-        out, row_m, row_z = _with_state(q, k, v, bias=bias, is_causal=is_causal, out_bnhd=True, **fwd_kwargs)
+        out, row_m, row_z = _with_state(q, k, v, bias=bias, is_causal=is_causal, out_bnhd=True, exact_row_max=False,
+                                        **fwd_kwargs)
         _save(ctx, (qkv,), out, bias, row_m, row_z, is_causal, bwd_kwargs)
         return out
 

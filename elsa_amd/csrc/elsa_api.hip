@@ -205,6 +205,7 @@ int run_phase(const elsa_fwd_args* a, const elsa_fwd_plan& pl, int q_start, int 
                     a->summary_dtype == a->dtype && a->partition_len % 64 == 0)
                        ? 1
                        : 0;
+    p.exact_max = a->exact_row_max ? 1 : 0;
     p.rows_pad = pl.q_chunk;
     hipError_t e = elsa::launch_phase1(p, a->dtype, pl.block_m, st);
     if (e != hipSuccess) return hip_fail(e, "phase1 launch");

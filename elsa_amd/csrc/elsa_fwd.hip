@@ -395,6 +395,7 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
 // moves), so its output is already score - m_run and p = exp2 of it, with no per-score
 // scale-and-subtract.
 constexpr float kLazyTau = 8.0f;
+constexpr float kLazySum = 256.0f;  // 2^kLazyTau
 
 // 2 waves per SIMD, except the 1- and 2-wave variants at D >= 64 (sequences of at most 64
 // keys): their register staging of a whole 64-key stage does not fit that budget.
@@ -710,7 +711,7 @@ void phase1_half_kernel(const Phase1Params p) {
 // from ph = 2i+2 on.
 // Measured (per-wave timestamps): the matrix phase takes about three times as long as the
 // vector phase, and the kernel is 5% faster than the two-waves-per-SIMD fold at 16K-64K keys.
-template <typename T, int DP, bool PRE>
+template <typename T, int DP, bool PRE, bool EXACT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void phase1_pp_kernel(const Phase1Params p) {
   using M = Mfma<T>;
@@ -869,68 +870,168 @@ void phase1_pp_kernel(const Phase1Params p) {
           for (int r = 0; r < 16; ++r)
             if (t0 + sub * 32 + key_of_reg(r, g) >= k_end) s[rt][sub][r] = kNegInf;
     }
-    float m_tile[RT];
-    bool raise = false;
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      float mx = kNegInf, mx1 = kNegInf;
-#pragma unroll
-      for (int sub = 0; sub < NSUB; ++sub)
-#pragma unroll
-        for (int r = 0; r < 16; r += 4) {
-          mx = fmaxf(fmaxf(mx, s[rt][sub][r]), s[rt][sub][r + 1]);
-          mx1 = fmaxf(fmaxf(mx1, s[rt][sub][r + 2]), s[rt][sub][r + 3]);
-        }
-      mx = wave_max_pair(fmaxf(mx, mx1));
-      if constexpr (PRE) {
-        m_tile[rt] = mx - negref[rt][0];  // the product started from -ref
-      } else {
-        m_tile[rt] = mx * cs;
-      }
-      m_true[rt] = fmaxf(m_true[rt], m_tile[rt]);
-      raise |= m_tile[rt] > m_run[rt] + kLazyTau;
-    }
-    if (__any(raise)) {
-#pragma unroll
+    if constexpr (EXACT) {
+      float m_tile[RT];
+      bool raise = false;
+  #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        const float m_new = fmaxf(m_run[rt], m_tile[rt]);
-        const float alpha = (m_run[rt] == kNegInf) ? 0.f : fast_exp2(m_run[rt] - m_new);
-        z_lane[rt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[rt][dt][r] *= alpha;
-        m_run[rt] = m_new;
+        float mx = kNegInf, mx1 = kNegInf;
+  #pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub)
+  #pragma unroll
+          for (int r = 0; r < 16; r += 4) {
+            mx = fmaxf(fmaxf(mx, s[rt][sub][r]), s[rt][sub][r + 1]);
+            mx1 = fmaxf(fmaxf(mx1, s[rt][sub][r + 2]), s[rt][sub][r + 3]);
+          }
+        mx = wave_max_pair(fmaxf(mx, mx1));
         if constexpr (PRE) {
-          // the scores are relative to the old reference: move them to the new one (a row still
-          // at -inf has only -inf scores and keeps reference 0)
-          const float ref = (m_new == kNegInf) ? 0.f : m_new;
-          const float shift = ref + negref[rt][0];
+          m_tile[rt] = mx - negref[rt][0];  // the product started from -ref
+        } else {
+          m_tile[rt] = mx * cs;
+        }
+        m_true[rt] = fmaxf(m_true[rt], m_tile[rt]);
+        raise |= m_tile[rt] > m_run[rt] + kLazyTau;
+      }
+      if (__any(raise)) {
+  #pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const float m_new = fmaxf(m_run[rt], m_tile[rt]);
+          const float alpha = (m_run[rt] == kNegInf) ? 0.f : fast_exp2(m_run[rt] - m_new);
+          z_lane[rt] *= alpha;
+  #pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+  #pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[rt][dt][r] *= alpha;
+          m_run[rt] = m_new;
+          if constexpr (PRE) {
+            // the scores are relative to the old reference: move them to the new one (a row still
+            // at -inf has only -inf scores and keeps reference 0)
+            const float ref = (m_new == kNegInf) ? 0.f : m_new;
+            const float shift = ref + negref[rt][0];
+  #pragma unroll
+            for (int sub = 0; sub < NSUB; ++sub)
+  #pragma unroll
+              for (int r = 0; r < 16; ++r) s[rt][sub][r] -= shift;
+  #pragma unroll
+            for (int r = 0; r < 16; ++r) negref[rt][r] = -ref;
+          }
+        }
+      }
+      // the row sums in phase1_half_kernel's order, so that both kernels give the same bits
+  #pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const float nm = (m_run[rt] == kNegInf) ? 0.f : -m_run[rt];
+        float zs = 0.f;
+  #pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub)
+  #pragma unroll
+          for (int j = 0; j < 2; ++j)
+  #pragma unroll
+            for (int t = 0; t < 8; ++t) {
+              const float pr = PRE ? fast_exp2(s[rt][sub][j * 8 + t]) : fast_exp2(fmaf(s[rt][sub][j * 8 + t], cs, nm));
+              pk[rt][sub][j][t] = static_cast<T>(pr);
+              zs += pr;
+            }
+        z_lane[rt] += zs;
+      }
+    } else {
+      // p in place of the scores and the lane's row sums, against the current reference.  A
+      // lane whose sum stays at or below 2^kLazyTau has no p above it, so the reference stands
+      // and the stage needs no row maximum.  Otherwise (and on the first stage) the scores are
+      // formed again from Ks[i % 2], which is rewritten only at the end of group 0's V_{i+1},
+      // and the stage raises the reference to its maximum as the exact path does.
+      float zsv[RT];
+      auto expo = [&]() {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const float nm = (m_run[rt] == kNegInf) ? 0.f : -m_run[rt];
+          float zs = 0.f;
 #pragma unroll
           for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s[rt][sub][r] -= shift;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) negref[rt][r] = -ref;
+            for (int r = 0; r < 16; ++r) {
+              const float pr = PRE ? fast_exp2(s[rt][sub][r]) : fast_exp2(fmaf(s[rt][sub][r], cs, nm));
+              s[rt][sub][r] = pr;
+              zs += pr;
+            }
+          zsv[rt] = zs;
         }
-      }
-    }
-    // the row sums in phase1_half_kernel's order, so that both kernels give the same bits
+      };
+      expo();
+      bool redo = false;
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const float nm = (m_run[rt] == kNegInf) ? 0.f : -m_run[rt];
-      float zs = 0.f;
+      for (int rt = 0; rt < RT; ++rt) redo |= !(zsv[rt] <= kLazySum) || m_run[rt] == kNegInf;
+      if (__any(redo)) {
+        const T* ks = Ks[i & 1];
 #pragma unroll
-      for (int sub = 0; sub < NSUB; ++sub)
+        for (int sub = 0; sub < NSUB; ++sub) {
+          const T* krow = ks + (sub * 32 + swap23(c)) * KS + g * 8;
+          F kf[NKK];
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+          for (int kk = 0; kk < NKK; ++kk) kf[kk] = *reinterpret_cast<const F*>(krow + kk * 16);
 #pragma unroll
-          for (int t = 0; t < 8; ++t) {
-            const float pr = PRE ? fast_exp2(s[rt][sub][j * 8 + t]) : fast_exp2(fmaf(s[rt][sub][j * 8 + t], cs, nm));
-            pk[rt][sub][j][t] = static_cast<T>(pr);
-            zs += pr;
+          for (int rt = 0; rt < RT; ++rt) {
+            if constexpr (PRE) {
+              s[rt][sub] = M::mma(kf[0], qf[rt][0], negref[rt]);
+            } else {
+              s[rt][sub] = M::mma(kf[0], qf[rt][0], f32x16{});
+            }
+#pragma unroll
+            for (int kk = 1; kk < NKK; ++kk) s[rt][sub] = M::mma(kf[kk], qf[rt][kk], s[rt][sub]);
           }
-      z_lane[rt] += zs;
+        }
+        if (t0 + KT > k_end) {
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+              for (int r = 0; r < 16; ++r)
+                if (t0 + sub * 32 + key_of_reg(r, g) >= k_end) s[rt][sub][r] = kNegInf;
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          float mx = kNegInf, mx1 = kNegInf;
+#pragma unroll
+          for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+            for (int r = 0; r < 16; r += 4) {
+              mx = fmaxf(fmaxf(mx, s[rt][sub][r]), s[rt][sub][r + 1]);
+              mx1 = fmaxf(fmaxf(mx1, s[rt][sub][r + 2]), s[rt][sub][r + 3]);
+            }
+          mx = wave_max_pair(fmaxf(mx, mx1));
+          const float m_tile = PRE ? mx - negref[rt][0] : mx * cs;
+          const float m_new = fmaxf(m_run[rt], m_tile);
+          const float alpha = (m_run[rt] == kNegInf) ? 0.f : fast_exp2(m_run[rt] - m_new);
+          z_lane[rt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[rt][dt][r] *= alpha;
+          m_run[rt] = m_new;
+          if constexpr (PRE) {
+            const float ref = (m_new == kNegInf) ? 0.f : m_new;
+            const float shift = ref + negref[rt][0];
+#pragma unroll
+            for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) s[rt][sub][r] -= shift;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) negref[rt][r] = -ref;
+          }
+        }
+        expo();
+      }
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        z_lane[rt] += zsv[rt];
+#pragma unroll
+        for (int sub = 0; sub < NSUB; ++sub)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int t = 0; t < 8; ++t) pk[rt][sub][j][t] = static_cast<T>(s[rt][sub][j * 8 + t]);
+      }
     }
     if (grp == 0) {
       static_for<0, NCH>([&](auto I) {
@@ -953,7 +1054,9 @@ void phase1_pp_kernel(const Phase1Params p) {
     const float z_raw = wave_sum_pair(z_lane[rt]);
     const int my_row = row0 + rt * 32 + c;
     if (my_row >= q_end) continue;
-    // renormalise to the exact row maximum (m_run <= m_true <= m_run + kLazyTau)
+    // renormalise to the exact row maximum (m_run <= m_true <= m_run + kLazyTau); the
+    // relaxed state keeps the reference m_run, at most kLazyTau below the maximum
+    if constexpr (!EXACT) m_true[rt] = m_run[rt];
     const float f = (m_true[rt] == kNegInf) ? 1.f : fast_exp2(m_run[rt] - m_true[rt]);
     const int64_t ridx = ((int64_t)kb * p.BH + bh) * p.rows_pad + (my_row - p.q_start);
     const int64_t orow = (int64_t)bh * p.N + my_row;
@@ -1160,11 +1263,21 @@ static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
       bool done = false;
       if constexpr (std::is_same<T, f16>::value) {
         if (p.prescale_q) {
-          hipLaunchKernelGGL((phase1_pp_kernel<T, DP, true>), g2, dim3(512), 0, st, p);
+          if (p.exact_max) {
+            hipLaunchKernelGGL((phase1_pp_kernel<T, DP, true, true>), g2, dim3(512), 0, st, p);
+          } else {
+            hipLaunchKernelGGL((phase1_pp_kernel<T, DP, true, false>), g2, dim3(512), 0, st, p);
+          }
           done = true;
         }
       }
-      if (!done) hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false>), g2, dim3(512), 0, st, p);
+      if (!done) {
+        if (p.exact_max) {
+          hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, true>), g2, dim3(512), 0, st, p);
+        } else {
+          hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, false>), g2, dim3(512), 0, st, p);
+        }
+      }
       return hipGetLastError();
     }
   }

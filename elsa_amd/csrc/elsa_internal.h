@@ -38,6 +38,10 @@ struct Phase1Params {
   // QK^T product in the base-2 domain (the reference's fp16 d64 fold without bias or
   // causal mask, attention_parallel_scan.py:257-259); otherwise fp32 scores are scaled
   int prescale_q;
+  // exact_max == 0: the row state may keep the lazy reference (at most kLazyTau below the row
+  // maximum, z relative to it) instead of the maximum; the fold then forms each stage's row
+  // maximum only where its partial sums show a score past the reference + kLazyTau
+  int exact_max;
   int64_t rows_pad;
   // direct != 0 (only with P == 1): apply Phase 2's finalize in the epilogue and write
   // out (the input dtype, layout os) and the row state instead of the summary

@@ -78,7 +78,8 @@ struct FwdState {
 };
 
 // elsa_fwd with row state on [B, H, N, D] operands (any layout the ABI accepts); out is
-// written as [B, N, H, D] memory when out_bnhd, else dense.
+// written as [B, N, H, D] memory when out_bnhd, else dense.  The state is the training
+// forward's: a reference within 8 below the row maximum, z relative to it.
 FwdState fwd_call(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& bias, bool causal,
                   int64_t summary_dtype, int64_t partition_len, int64_t q_chunk, bool out_bnhd) {
   const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
@@ -109,6 +110,7 @@ FwdState fwd_call(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
   a.k_layout = layout_of(k);
   a.v_layout = layout_of(v);
   a.out_layout = layout_of(st.out);
+  a.exact_row_max = 0;  // the state only feeds the backward (row_m + log2 row_z)
   elsa_fwd_plan plan;
   check(elsa_fwd_plan_get(&a, &plan), "elsa_fwd_plan_get");
   const at::Tensor ws = bytes(q, plan.workspace_bytes);

@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define ELSA_ABI_VERSION 3
+#define ELSA_ABI_VERSION 4
 
 typedef enum elsa_dtype { ELSA_F16 = 0, ELSA_BF16 = 1, ELSA_F32 = 2 } elsa_dtype;
 
@@ -99,6 +99,13 @@ typedef struct elsa_fwd_args {
   void* workspace;
   size_t workspace_bytes;
   elsa_layout q_layout, k_layout, v_layout, out_layout; /* zero = dense [B,H,N,D]  */
+  /* Row state.  1: row_m is each row's maximum base-2 score and row_z the sum of
+   * exp2(score - row_m), as twopass_attention_with_state returns them (attention_bwd.py:77-185).
+   * 0: row_m may be any reference from that maximum - 8 up to the maximum, with row_z relative
+   * to it: the same log-sum-exp row_m + log2(row_z), which is all elsa_bwd reads (the training
+   * path).  The fp16/bf16 d64 fold then forms a 64-key stage's row maximum only where the
+   * stage's partial sums show a score past the reference + 8. */
+  int32_t exact_row_max;
 } elsa_fwd_args;
 
 typedef struct elsa_fwd_plan {

@@ -39,7 +39,7 @@ def test_torch_module_loads_with_the_library_abi():
 
 def test_abi_version_and_struct_sizes():
     lib = _lib.load()
-    assert lib.elsa_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.elsa_abi_version() == _lib.ABI_VERSION == 4
     for which, st in _lib._STRUCTS.items():
         assert lib.elsa_struct_size(which) == ctypes.sizeof(st)
 

@@ -213,3 +213,52 @@ def test_inference_forward(case):
     describe(f"  out {info}")
     if n <= 8192 and not causal:  # the spot check's own bars against the exact output
         assert info["vs_exact_beyond_half_ulp"] <= (1e-5 if dt == "fp32" else 5e-3)
+
+
+# The training entry point (twopass_attention_train, the call the reference's benchmarks/bench_bwd.py
+# times): its forward keeps a relaxed row state wherever the ping-pong fold runs (fp16/bf16, d64,
+# non-causal, unbiased, partitions of at least 1024 keys): a reference m at most 8 below the row
+# maximum and z relative to it, the same log-sum-exp.  "spikes" scales two late keys so that their
+# stages must raise the reference (the fold's rare path) long after the first stage.
+TRAIN = [
+    ((1, 8, 16384, 64), "fp16", None, None),   # the north star's step (2 partitions of 8192 keys)
+    ((1, 8, 8192, 64), "fp16", None, None),
+    ((1, 4, 4096, 64), "fp16", "spikes", 1024),
+    ((2, 8, 4097, 64), "fp16", None, 2048),    # ragged: a last partition of one key, its stage masked
+    ((2, 16, 2048, 64), "bf16", None, 1024),
+]
+
+
+@pytest.mark.parametrize("case", TRAIN, ids=[f"{c[0]}-{c[1]}-{c[2] or 'randn'}-bn{c[3]}" for c in TRAIN])
+def test_train_entry_point_relaxed_state(case):
+    from elsa_amd.attention_bwd import _with_state
+
+    shape, dt, fill, bn = case
+    b, h, n, d = shape
+    describe(f"twopass_attention_train {shape} {dt} {fill or 'randn'} block_n={bn}")
+    q, k, v, do = _draw(shape, dt, seed=2027)
+    if fill == "spikes":
+        k[:, :, n - 700] *= 8
+        k[:, :, n - 90] *= 12
+    plan = forward_plan(q, is_causal=False, block_n=bn)
+    assert plan["partition_len"] >= 1024 and plan["block_m"] == 256, plan  # the ping-pong fold's routing
+    qd, kd, vd = (x.cuda().requires_grad_() for x in (q, k, v))
+    out = elsa_amd.twopass_attention_train(qd, kd, vd, block_n=bn)
+    dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), do.cuda())
+    # the relaxed state against the exact one on the same inputs and plan
+    with torch.no_grad():
+        _, m_e, z_e = elsa_amd.twopass_attention_with_state(qd, kd, vd, block_n=bn)
+        _, m_r, z_r = _with_state(qd, kd, vd, block_n=bn, exact_row_max=False)
+    torch.cuda.synchronize()
+    m_e, z_e, m_r, z_r = (_np(t.cpu()) for t in (m_e, z_e, m_r, z_r))
+    assert np.isfinite(m_r).all() and (z_r > 0).all()
+    assert (m_r <= m_e + 1e-5 * np.maximum(1.0, np.abs(m_e))).all() and (m_r >= m_e - 8.0 - 1e-5).all()
+    lse_e, lse_r = m_e + np.log2(z_e), m_r + np.log2(z_r)
+    err = np.abs(lse_r - lse_e).max()
+    describe(f"  relaxed state: max |LSE relaxed - LSE exact| = {err:.3e}, "
+             f"m below the maximum by up to {np.max(m_e - m_r):.3f}")
+    assert err <= 2e-5 * max(1.0, np.abs(lse_e).max())
+    got = [out.detach().float().cpu(), None, None] + [t.float().cpu() for t in (dq, dk, dv)]
+    part, micro = O.reference_routing(n, d, dt, training=True, is_causal=False)
+    heads = range(b * h) if b * h * n * n <= 8 * 4096 * 4096 else [0, b * h - 1]
+    _check_full_heads(q, k, v, do, got, dt, False, heads, part, micro)
