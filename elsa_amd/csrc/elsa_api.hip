@@ -372,6 +372,12 @@ elsa::BwdParams bwd_params(const elsa_bwd_args* a) {
   p.d_row = reinterpret_cast<float*>(base);
   p.lse_row = reinterpret_cast<float*>(base + align256(rows * 4));
   p.lse_lo = reinterpret_cast<float*>(base + 2 * align256(rows * 4));
+  p.dp = elsa::pad_head_dim(a->head_dim);
+  p.split = elsa::bwd_splits(a->dtype, p.dp, p.BH, p.N, a->bias.ptr != nullptr);
+  // rows (dK/dV) or keys (dq) per range: whole 64-row stages
+  p.split_len = p.split > 1 ? (int)((((int64_t)p.N + p.split - 1) / p.split + 63) / 64 * 64) : p.N;
+  p.part = p.split > 1 ? reinterpret_cast<float*>(base + 3 * align256(rows * 4)) : nullptr;
+  p.part_stride = (int64_t)(align256((size_t)p.split * rows * p.dp * 4) / 4);
   const int H = a->heads, N = a->seq_len, D = a->head_dim;
   resolve_layout(a->q_layout, H, N, D, p.qs);
   resolve_layout(a->k_layout, H, N, D, p.ks);
@@ -508,10 +514,20 @@ int elsa_phase2(const elsa_fwd_args* a, int32_t q_start, int32_t q_len, void* st
   return run_phase(a, pl, q_start, q_len, static_cast<hipStream_t>(stream), 2);
 }
 
+// fp32 partials of a split backward (dq, dK, dV): split * rows * dp floats each
+static size_t bwd_part_bytes(const elsa_bwd_args* a) {
+  const int dp = elsa::pad_head_dim(a->head_dim);
+  const int split = elsa::bwd_splits(a->dtype, dp, (int64_t)a->batch * a->heads, a->seq_len, a->bias.ptr != nullptr);
+  if (split <= 1) return 0;
+  const size_t rows = (size_t)a->batch * a->heads * a->seq_len;
+  return 3 * align256((size_t)split * rows * dp * 4);
+}
+
 size_t elsa_bwd_workspace_bytes(const elsa_bwd_args* a) {
   if (!a || a->batch <= 0 || a->heads <= 0 || a->seq_len <= 0) return 0;
   const size_t rows = (size_t)a->batch * a->heads * a->seq_len;
-  return 3 * align256(rows * 4);  // D, LSE2 and LSE2's low part, one float per row each
+  // D, LSE2 and LSE2's low part, one float per row each; then a split backward's partials
+  return 3 * align256(rows * 4) + bwd_part_bytes(a);
 }
 
 int elsa_bwd(const elsa_bwd_args* a, void* stream) { return elsa_bwd_stage(a, -1, stream); }

@@ -531,6 +531,11 @@ void bwd_dq_half_kernel(const BwdParams p) {
     live[rt] = ok && lse[rt] < __builtin_huge_valf();
   }
   const int k_end = p.causal ? wg_last + 1 : p.N;
+  // split (the 4-wave one-tile kernel only): this work-group's keys [k_lo, k_hi), whole 64-key
+  // stages (one range when unsplit)
+  constexpr bool CAN_SPLIT = RT == 1 && WAVES == 4 && !HAS_BIAS && DP <= 64;
+  const int k_lo = CAN_SPLIT ? min(k_end, wg.z * p.split_len) : 0;
+  const int k_hi = CAN_SPLIT ? min(k_end, k_lo + p.split_len) : k_end;
   // -D of this lane's row: the dP^T product starts from it and yields dP - D directly.  The
   // 16 registers per row tile of that constant would spill in the bias, D = 128 and two-tile
   // variants, which subtract D from each score instead.
@@ -582,7 +587,7 @@ static_for<0, NCH>([&](auto I) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) acc[rt][dt] = f32x16{};
 
-  const int ntiles = (k_end + KT - 1) / KT;
+  const int ntiles = (k_hi - k_lo + KT - 1) / KT;
   // stage keys [t0, t0 + KT) from LDS buffer buf into the dQ accumulators
   auto compute = [&](int buf, int t0) __attribute__((always_inline)) {
     if (!p.causal || t0 <= row0 + ROWS_W - 1) {
@@ -659,13 +664,13 @@ static_for<0, NCH>([&](auto I) {
     // second register set spills at two waves per SIMD, and one wave per SIMD is slower still
     // (1.64 against 1.87-2.07 ms), so that width keeps one stage of prefetch, and so does the
     // two-tile variant (255 VGPRs with one set)
-    gload(0, S0);
+    gload(k_lo, S0);
     sstore(0, S0);
-    if (ntiles > 1) gload(KT, S1);
+    if (ntiles > 1) gload(k_lo + KT, S1);
     __syncthreads();
     auto step = [&](int it, auto NEXT, auto FREE) __attribute__((always_inline)) {
       const int buf = it & 1;
-      const int t0 = it * KT;
+      const int t0 = k_lo + it * KT;
       if (it + 2 < ntiles) gload(t0 + 2 * KT, FREE);
       compute(buf, t0);
       if (it + 1 < ntiles) sstore(buf ^ 1, NEXT);
@@ -676,12 +681,12 @@ static_for<0, NCH>([&](auto I) {
       if (it + 1 < ntiles) step(it + 1, S0, S1);
     }
   } else {
-    gload(0, S0);
+    gload(k_lo, S0);
     sstore(0, S0);
     __syncthreads();
     for (int it = 0; it < ntiles; ++it) {
       const int buf = it & 1;
-      const int t0 = it * KT;
+      const int t0 = k_lo + it * KT;
       const bool has_next = it + 1 < ntiles;
       if (has_next) gload(t0 + KT, S0);
       compute(buf, t0);
@@ -693,6 +698,18 @@ static_for<0, NCH>([&](auto I) {
   for (int rt = 0; rt < RT; ++rt) {
     const int my_row = row0 + rt * 32 + c;
     if (my_row >= p.N) continue;
+    if (CAN_SPLIT && p.split > 1) {  // this key range's unscaled dQ, fp32
+      float* dst = p.part + (((int64_t)wg.z * p.BH + bh) * p.N + my_row) * p.dp;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int d = dt * 32 + q4 * 8 + 4 * g;
+          *reinterpret_cast<f32x4*>(dst + d) =
+              f32x4{acc[rt][dt][4 * q4], acc[rt][dt][4 * q4 + 1], acc[rt][dt][4 * q4 + 2], acc[rt][dt][4 * q4 + 3]};
+        }
+      continue;
+    }
     T* out = static_cast<T*>(p.dq) + bi * p.dqs[0] + hi * p.dqs[1] + (int64_t)my_row * p.dqs[2];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
@@ -814,8 +831,12 @@ static_for<0, NCH>([&](auto I) {
     }
   };
 
-  const int r_begin = p.causal ? (wg_key0 / RTS) * RTS : 0;
-  const int ntiles = (p.N - r_begin + RTS - 1) / RTS;
+  // split (the 4-wave one-tile kernel only): this work-group's rows [r_lo, r_hi), whole 64-row
+  // stages (one range when unsplit)
+  constexpr bool CAN_SPLIT = KRT == 1 && WAVES == 4 && !HAS_BIAS && DP <= 64;
+  const int r_lo = max(p.causal ? (wg_key0 / RTS) * RTS : 0, CAN_SPLIT ? wg.z * p.split_len : 0);
+  const int r_hi = CAN_SPLIT ? min(p.N, wg.z * p.split_len + p.split_len) : p.N;
+  const int ntiles = r_hi > r_lo ? (r_hi - r_lo + RTS - 1) / RTS : 0;
   // stage rows [t0, t0 + RTS) from LDS buffer buf into the dK / dV accumulators
   auto compute = [&](int buf, int t0) __attribute__((always_inline)) {
     if (!p.causal || t0 + RTS - 1 >= key0) {
@@ -918,13 +939,13 @@ static_for<0, NCH>([&](auto I) {
   const auto S1 = std::integral_constant<int, 1>{};
   // global loads two stages ahead: stage it + 2 goes into the register set that stage it
   // left, while stage it + 1 waits in the other one for the end of this stage
-  gload(r_begin, S0);
+  gload(r_lo, S0);
   sstore(0, S0);
-  if (ntiles > 1) gload(r_begin + RTS, S1);
+  if (ntiles > 1) gload(r_lo + RTS, S1);
   __syncthreads();
   auto step = [&](int it, auto NEXT, auto FREE) __attribute__((always_inline)) {
     const int buf = it & 1;
-    const int t0 = r_begin + it * RTS;
+    const int t0 = r_lo + it * RTS;
     if (it + 2 < ntiles) gload(t0 + 2 * RTS, FREE);
     compute(buf, t0);
     if (it + 1 < ntiles) sstore(buf ^ 1, NEXT);
@@ -938,6 +959,21 @@ static_for<0, NCH>([&](auto I) {
   for (int kt = 0; kt < KRT; ++kt) {
     const int my_key = key0 + kt * 32 + c;
     if (my_key >= p.N) continue;
+    if (CAN_SPLIT && p.split > 1) {  // this row range's unscaled dK and dV, fp32
+      float* dkp = p.part + p.part_stride + (((int64_t)wg.z * p.BH + bh) * p.N + my_key) * p.dp;
+      float* dvp = dkp + p.part_stride;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int d = dt * 32 + q4 * 8 + 4 * g;
+          *reinterpret_cast<f32x4*>(dkp + d) = f32x4{dk[kt][dt][4 * q4], dk[kt][dt][4 * q4 + 1], dk[kt][dt][4 * q4 + 2],
+                                                     dk[kt][dt][4 * q4 + 3]};
+          *reinterpret_cast<f32x4*>(dvp + d) = f32x4{dv[kt][dt][4 * q4], dv[kt][dt][4 * q4 + 1], dv[kt][dt][4 * q4 + 2],
+                                                     dv[kt][dt][4 * q4 + 3]};
+        }
+      continue;
+    }
     T* okp = static_cast<T*>(p.dk) + bi * p.dks[0] + hi * p.dks[1] + (int64_t)my_key * p.dks[2];
     T* ovp = static_cast<T*>(p.dv) + bi * p.dvs[0] + hi * p.dvs[1] + (int64_t)my_key * p.dvs[2];
 #pragma unroll
@@ -1174,6 +1210,61 @@ hipError_t launch_zero_fill(float* dst, int64_t n, hipStream_t st) {
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------ split backward
+int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias) {
+  if (dtype == ELSA_F32 || bias || dp > 64) return 1;
+  const int64_t wgs = bh * ((n + 127) / 128);  // the unsplit 4-wave grid
+  int s = 1;
+  while (s < 8 && wgs * s < 512 && n / (2 * s) >= 256) s *= 2;
+  return s;
+}
+
+// out[b, h, n, d] = scale * sum over the split ranges of part[z][b*H + h][n][d], 4 head-dim
+// elements per thread (head dims are multiples of 8); grid y picks one of up to two such sums
+struct CombineOut {
+  const float* part;
+  void* out;
+  int64_t os[3];
+  float scale;
+};
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_combine_kernel(CombineOut c0, CombineOut c1, int split, int64_t sstride,
+                                                          int H, int N, int D, int dp) {
+  const CombineOut& cj = blockIdx.y ? c1 : c0;
+  const float* __restrict__ part = cj.part;
+  T* __restrict__ out = static_cast<T*>(cj.out);
+  const int64_t o0 = cj.os[0], o1 = cj.os[1], o2 = cj.os[2];
+  const float scale = cj.scale;
+  const int c4 = D / 4;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = i / c4;  // over B*H*N
+  if (row >= sstride / dp) return;
+  const int d = (int)(i - row * c4) * 4;
+  const float* src = part + row * dp + d;
+  f32x4 acc = *reinterpret_cast<const f32x4*>(src);
+  for (int z = 1; z < split; ++z) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(src + z * sstride);
+    acc[0] += v[0];
+    acc[1] += v[1];
+    acc[2] += v[2];
+    acc[3] += v[3];
+  }
+  const int64_t bh = row / N, n = row - bh * N;
+  typedef T t4 __attribute__((ext_vector_type(4)));
+  const t4 o = {static_cast<T>(acc[0] * scale), static_cast<T>(acc[1] * scale), static_cast<T>(acc[2] * scale),
+                static_cast<T>(acc[3] * scale)};
+  *reinterpret_cast<t4*>(out + (bh / H) * o0 + (bh % H) * o1 + n * o2 + d) = o;
+}
+
+template <typename T>
+static hipError_t combine_launch(const BwdParams& p, const CombineOut& c0, const CombineOut* c1, hipStream_t st) {
+  const int64_t rows = (int64_t)p.BH * p.N;
+  const int64_t threads = rows * (p.D / 4);
+  hipLaunchKernelGGL(bwd_combine_kernel<T>, dim3((unsigned)((threads + 255) / 256), c1 ? 2u : 1u), dim3(256), 0, st,
+                     c0, c1 ? *c1 : c0, p.split, rows * p.dp, p.H, p.N, p.D, p.dp);
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ launchers
 template <typename T>
 static hipError_t pre_launch(const BwdParams& p, hipStream_t st) {
@@ -1195,6 +1286,27 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
     constexpr int R = 1;  // one 32-wide tile per wave: 2 waves per SIMD beat wider tiles at 1
     const dim3 grid((p.N + 32 * R * W - 1) / (32 * R * W), p.BH);
+    if constexpr (!B && DP <= 64) {
+      if (p.split > 1) {
+        // an under-filled grid (short sequences, few heads): the key (dq) or row (dK/dV) loop cut
+        // into p.split ranges over grid z, fp32 partials summed by a combine launch
+        const dim3 gs(grid.x, grid.y, (unsigned)p.split);
+        if (stage < 0 || stage == 1) {
+          hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, W, false>), gs, dim3(64 * W), 0, st, p);
+          if ((e = hipGetLastError()) != hipSuccess) return e;
+          const CombineOut cq{p.part, p.dq, {p.dqs[0], p.dqs[1], p.dqs[2]}, p.scale};
+          if ((e = combine_launch<T>(p, cq, nullptr, st)) != hipSuccess) return e;
+        }
+        if (stage < 0 || stage == 2) {
+          hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, W, false>), gs, dim3(64 * W), 0, st, p);
+          if ((e = hipGetLastError()) != hipSuccess) return e;
+          const CombineOut ck{p.part + p.part_stride, p.dk, {p.dks[0], p.dks[1], p.dks[2]}, p.scale};
+          const CombineOut cv{p.part + 2 * p.part_stride, p.dv, {p.dvs[0], p.dvs[1], p.dvs[2]}, 1.f};
+          e = combine_launch<T>(p, ck, &cv, st);
+        }
+        return e;
+      }
+    }
     if (stage < 0 || stage == 1) {
       // dq with two 32-row tiles per wave (256-row work-groups): each K/V fragment read from LDS
       // feeds both tiles, halving the LDS reads per MFMA.  Non-causal, unbiased, D <= 64, and only

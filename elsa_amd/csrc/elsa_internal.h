@@ -102,7 +102,19 @@ struct BwdParams {
   float scale_log2;  // scale * log2(e)
   // element strides (batch, head, row) of q, k, v, out, dout and of dq, dk, dv
   int64_t qs[3], ks[3], vs[3], os[3], gs[3], dqs[3], dks[3], dvs[3];
+  // split > 1 (bwd_splits): the fp16/bf16 dq and dK/dV kernels cut their key (dq) or row (dK/dV)
+  // loop into `split` ranges of split_len (a multiple of 64) over grid z, and write unscaled fp32
+  // partials, [split][BH][N][dp] each for dq, dK and dV from part on; a combine kernel sums them
+  int split, split_len, dp;
+  float* part;
+  int64_t part_stride;  // floats from the dq partials to the dK ones and from those to the dV ones
 };
+
+// Ranges the fp16/bf16 backward cuts its loops into when its unsplit grid (128 rows or keys per
+// work-group) leaves the chip under-filled: 1 (no split) unless fewer than 512 work-groups, then
+// doubled while that stays short of 512 and every range keeps at least 256 rows.  fp32, biased
+// calls and head dims above 64 keep 1.
+int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias);
 
 // stage < 0: preprocess, dq and dk/dv; 0: preprocess only; 1: dq only; 2: dk/dv only.
 hipError_t launch_bwd(const BwdParams& p, int dtype, int stage, hipStream_t stream);

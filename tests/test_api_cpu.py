@@ -287,3 +287,33 @@ def test_canonical_bias_cpu():
         _canonical_bias(torch.zeros(3, 3, 8, 8), batch=2, heads=3, seq_len=8, device=dev)
     with pytest.raises(ValueError, match="last dims"):
         _canonical_bias(torch.zeros(8, 7), batch=2, heads=3, seq_len=8, device=dev)
+
+
+def _align256(x):
+    return (x + 255) // 256 * 256
+
+
+@pytest.mark.parametrize("n,bh,dtype,d,split", [
+    (1024, (1, 8), _lib.ELSA_F16, 64, 4),    # 64 four-wave work-groups: four 256-row ranges
+    (4096, (1, 8), _lib.ELSA_F16, 64, 2),    # 256 work-groups: two ranges fill the chip twice
+    (2048, (1, 8), _lib.ELSA_BF16, 64, 4),
+    (1025, (8, 3), _lib.ELSA_F16, 64, 4),    # ViT-T at 512 px
+    (2305, (8, 3), _lib.ELSA_F16, 32, 2),
+    (16384, (1, 8), _lib.ELSA_F16, 64, 1),   # the north star's grid is full
+    (197, (8, 3), _lib.ELSA_F16, 64, 1),     # ranges would fall below 256 rows
+    (1024, (1, 8), _lib.ELSA_F32, 64, 1),    # fp32 and d = 128 keep their unsplit kernels
+    (1024, (1, 8), _lib.ELSA_F16, 128, 1),
+])
+def test_bwd_workspace_holds_the_split_partials(n, bh, dtype, d, split):
+    """Short sequences with few heads cut the backward's key (dq) and row (dK/dV) loops into ranges
+    over extra work-groups; the workspace then holds their fp32 partials of dq, dK and dV."""
+    lib = _lib.load()
+    b = _lib.BwdArgs()
+    b.batch, b.heads, b.seq_len, b.head_dim, b.dtype = bh[0], bh[1], n, d, dtype
+    rows = bh[0] * bh[1] * n
+    part = 3 * _align256(split * rows * d * 4) if split > 1 else 0
+    assert lib.elsa_bwd_workspace_bytes(ctypes.byref(b)) == 3 * _align256(rows * 4) + part
+    # a bias keeps the unsplit kernels (dS may be stored per score)
+    bias = torch.zeros(1)
+    b.bias = _lib.bias_desc(bias, (0, 0, n, 1))
+    assert lib.elsa_bwd_workspace_bytes(ctypes.byref(b)) == 3 * _align256(rows * 4)

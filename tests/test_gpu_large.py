@@ -138,6 +138,8 @@ FULL = [
     ((4, 32, 1024, 64), "fp16", False),  # 512 dq work-groups of 256 rows: the two-tile dq kernel
     ((2, 64, 1024, 64), "bf16", False),
     ((4, 32, 1024, 64), "fp16", True),   # causal: the 8-wave dq and dK/dV work-groups
+    ((1, 8, 2048, 64), "bf16", False),   # the split backward (four key / row ranges, fp32 partials)
+    ((2, 4, 2048, 32), "fp16", True),    # the same at d = 32, causal
 ]
 
 
