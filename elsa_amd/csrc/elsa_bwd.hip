@@ -532,8 +532,10 @@ void bwd_dq_half_kernel(const BwdParams p) {
   }
   const int k_end = p.causal ? wg_last + 1 : p.N;
   // split (the 4-wave one-tile kernel only): this work-group's keys [k_lo, k_hi), whole 64-key
-  // stages (one range when unsplit)
-  constexpr bool CAN_SPLIT = RT == 1 && WAVES == 4 && !HAS_BIAS && DP <= 64;
+  // stages (one range when unsplit).  D = 128 never splits (bwd_splits) but keeps these run-time
+  // bounds: with constant ones its register allocation spilled (20 bytes per lane, 468 biased;
+  // 16K dq 1.698 -> 1.653 ms without)
+  constexpr bool CAN_SPLIT = RT == 1 && WAVES == 4 && (DP == 128 || (!HAS_BIAS && DP <= 64));
   const int k_lo = CAN_SPLIT ? min(k_end, wg.z * p.split_len) : 0;
   const int k_hi = CAN_SPLIT ? min(k_end, k_lo + p.split_len) : k_end;
   // -D of this lane's row: the dP^T product starts from it and yields dP - D directly.  The
