@@ -73,6 +73,18 @@ def test_plan_north_star_routing():
     assert p.workspace_bytes >= rows * (8 + 64 * 2)
 
 
+@pytest.mark.parametrize("n,dtype,d,causal,parts,part", [
+    (4096, _lib.ELSA_F16, 64, 0, 4, 1024),   # the ping-pong fold's partitions of >= 1024 keys
+    (4096, _lib.ELSA_BF16, 64, 0, 4, 1024),
+    (2048, _lib.ELSA_F16, 64, 0, 4, 512),    # 2K keeps four partitions of 512 (the 4-wave fold)
+    (4096, _lib.ELSA_F16, 64, 1, 8, 512),    # causal keeps the 4-wave fold's partitions
+    (4096, _lib.ELSA_F16, 32, 0, 8, 512),
+])
+def test_plan_ping_pong_partitions_from_4k(n, dtype, d, causal, parts, part):
+    rc, p = _plan(_args(n=n, dtype=dtype, d=d, causal=causal))
+    assert rc == 0 and (p.partitions, p.partition_len) == (parts, part)
+
+
 @pytest.mark.parametrize("n,bh,d", [(49, (8, 3), 32), (197, (8, 3), 64), (1024, (1, 8), 64), (65536, (1, 8), 64),
                                     (4097, (8, 3), 64), (300, (1, 2), 128)])
 def test_plan_partitions_cover_sequence(n, bh, d):
