@@ -426,7 +426,7 @@ void phase1_half_kernel(const Phase1Params p) {
   // prescaled fold is never causal: no registers spent on it there)
   const bool lpt = !PRE && p.causal && p.q_start == 0 && p.q_len == p.N && p.part_len % BM == 0;
   const WgCoord wg = lpt ? causal_longest_first((int)gridDim.x, p.BH, p.P, p.part_len / BM)
-                         : (PRE ? xcd_order() : phase1_order(p.causal));
+                         : (PRE ? panel_order() : phase1_order(p.causal));
   const int bh = wg.y, kb = wg.z;
   const int q_end = p.q_start + p.q_len;
   const int wg_row0 = p.q_start + wg.x * BM;
@@ -727,7 +727,7 @@ void phase1_pp_kernel(const Phase1Params p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31, g = lane >> 5;
   const int grp = wave >> 2;
-  const WgCoord wg = xcd_order();
+  const WgCoord wg = panel_order();
   const int bh = wg.y, kb = wg.z;
   const int q_end = p.q_start + p.q_len;
   const int wg_row0 = p.q_start + wg.x * BM;

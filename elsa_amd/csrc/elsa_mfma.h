@@ -178,9 +178,23 @@ __device__ inline WgCoord xcd_order() {
   const int gx = gridDim.x, gy = gridDim.y, l = xcd_linear();
   return {l % gx, (l / gx) % gy, l / (gx * gy)};
 }
-// Phase 1 order (grid x = row block, y = head, z = K partition).  Non-causal: the XCD
-// order (row blocks fastest), so the workgroups resident on one XCD share one K/V
-// partition panel in its L2: Phase 1 then fetches its algorithmic bytes (Q once per
+// Non-causal Phase 1 (grid x = row block, y = head, z = K partition) with the panels (head,
+// partition) dealt to the XCDs in turn, each panel whole: the dispatcher sends workgroup L to
+// XCD L % 8, and the j-th workgroup of an XCD (j = L / 8) takes row block j % gx of panel
+// L % 8 + 8 (j / gx), panel = head + gy * partition.  A short last partition then spreads its
+// panels over all XCDs instead of leaving the last XCDs idle (B1 H8 N16K with 8190-key
+// partitions: 96 workgroups of the full partitions on each of five XCDs against 64 on
+// every XCD).  Panel counts that are not a multiple of 8 keep xcd_order.
+__device__ inline WgCoord panel_order() {
+  const int gx = gridDim.x, gy = gridDim.y, npan = gy * gridDim.z;
+  if (npan & 7) return xcd_order();
+  const int lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const int j = lin >> 3, pan = (lin & 7) + 8 * (j / gx);
+  return {j % gx, pan % gy, pan / gy};
+}
+// Phase 1 order (grid x = row block, y = head, z = K partition).  Non-causal: panel_order
+// (row blocks fastest, whole panels per XCD), so the workgroups resident on one XCD share one
+// K/V partition panel in its L2: Phase 1 then fetches its algorithmic bytes (Q once per
 // partition, K and V once; 101 MB at B1 H8 N16K d64 with 4 partitions), where a
 // partition-fastest order fetched 244 MB in the same time.  Causal: the work of a row block
 // grows with its index and vanishes for partitions past it; there the dispatcher's own
@@ -188,7 +202,7 @@ __device__ inline WgCoord xcd_order() {
 // start first.
 __device__ inline WgCoord phase1_order(bool causal) {
   if (causal) return {(int)gridDim.x - 1 - (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
-  return xcd_order();
+  return panel_order();
 }
 
 // Causal Phase 1 over the whole sequence (grid nrb row blocks x BH heads x P partitions, rpp =
