@@ -9,7 +9,9 @@ non-causal, synthetic N(0,1) q/k/v/dO (seed 2026) resident in HBM.
 Prints ONE JSON line.  ``value`` is the algorithmic fwd+bwd throughput
 (3.5 * 4*B*H*N^2*d flop per step, recompute not counted).  ``kernels`` holds each
 kernel's HIP-event average on the launch stream; ``roofline`` is computed for the
-kernel with the largest share of the step.  ``cpu_baseline`` times BASELINE config 1
+kernel with the largest share of the step.  ``baseline_configs`` times the other shapes of
+BASELINE configs 2 and 3 (B1 H8 d64: fp16 and fp32 at 1K-64K, causal fp16 at 197-32K) the same
+way, each with its training-step wall clock and a sampled fp64 check.  ``cpu_baseline`` times BASELINE config 1
 (B1 H8 N1024 d64 fp32 forward) through the pure-PyTorch restatement of the reference's
 monoid scan (oracle/torch_scan.py) on the host cores, with a row sample of this step's
 own work beside it.
@@ -66,6 +68,10 @@ def _args():
                     help="ViT-Tiny image sizes of the fp32 fields (empty: skip)")
     ap.add_argument("--swin-img-fp32", type=int, nargs="*", default=[224, 384, 512],
                     help="Swin-Tiny image sizes of the fp32 fields (empty: skip)")
+    # BASELINE configs 2 and 3 beside the main line: B1 H8 d64 fp16/fp32 1K-64K, causal fp16 197-32K
+    ap.add_argument("--configs", dest="configs", action="store_true", default=True)
+    ap.add_argument("--no-configs", dest="configs", action="store_false")
+    ap.add_argument("--config-steps", type=int, default=10, help="timed iterations per baseline_configs case")
     ap.add_argument("--vit-batch", type=int, default=8, help="image batch of the ViT-T / Swin-T fields")
     ap.add_argument("--vit-steps", type=int, default=10, help="timed iterations of the ViT-T / Swin-T fields")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -169,6 +175,145 @@ def _mfma_ceiling(args, lib, dev, stream) -> float:
     return tflops
 
 
+
+def _kernel_ms(lib, stream, q, k, v, do, causal, block_n, steps):
+    """HIP-event average of each hot-path launch set on ``stream``, through the C ABI.
+
+    Phase 1 + Phase 2 run the training forward (the relaxed row state the backward reads); the
+    three backward stages run on that forward's output and row state.  Returns (ms by kernel,
+    the forward plan, the forward output)."""
+    import torch
+
+    from elsa_amd import _lib
+    from elsa_amd.attention import _BiasMeta, _make_fwd_args, forward_plan
+    from elsa_amd.attention_bwd import _attach_workspace, _bwd_args
+
+    B, H, N, D = q.shape
+    dev = q.device
+    sh = stream.cuda_stream
+    plan = forward_plan(q, is_causal=causal, block_n=block_n)
+    out = torch.empty_like(q)
+    rm = torch.empty((B * H, N), device=dev, dtype=torch.float32)
+    rz = torch.empty_like(rm)
+    fa = _make_fwd_args(q, k, v, out, rm, rz, _BiasMeta(None, 0, 0, 0, 0, False), is_causal=causal,
+                        summary_dtype=q.dtype, partition_len=block_n, q_chunk=None, scale=1.0 / math.sqrt(D),
+                        exact_row_max=False)
+    ws_f = torch.empty(plan["workspace_bytes"], dtype=torch.uint8, device=dev)
+    fa.workspace, fa.workspace_bytes = ws_f.data_ptr(), plan["workspace_bytes"]
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ba = _bwd_args(q, k, v, out, do, rm, rz, dq, dk, dv, _BiasMeta(None, 0, 0, 0, 0, False), is_causal=causal,
+                   scale=1.0 / math.sqrt(D))
+    ws_b = _attach_workspace(lib, ba, dev)
+    qc = plan["q_chunk"]
+    chunks = [(s_, min(qc, N - s_)) for s_ in range(0, N, qc)]
+
+    launches = {
+        "phase1_fold": lambda: [lib.elsa_phase1(ctypes.byref(fa), s_, n_, sh) for s_, n_ in chunks],
+        "phase2_merge": lambda: [lib.elsa_phase2(ctypes.byref(fa), s_, n_, sh) for s_, n_ in chunks],
+        "bwd_preprocess": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 0, sh)],
+        "bwd_dq": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 1, sh)],
+        "bwd_dkdv": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 2, sh)],
+    }
+    kern_ms = {}
+    for name, fn in launches.items():
+        for rc in fn():
+            _lib.check(rc, name)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        kern_ms[name] = e0.elapsed_time(e1) / steps
+    del ws_f, ws_b, dq, dk, dv
+    return kern_ms, plan, out
+
+
+def _sampled_max_abs(q, k, v, out, causal, nrows=16, seed=0):
+    """max |out - softmax(q k^T / sqrt(d)) v| over ``nrows`` sampled query rows, fp64 on the CPU."""
+    import numpy as np
+
+    N, D = q.shape[2], q.shape[3]
+    rows = np.random.default_rng(seed).choice(N, min(nrows, N), replace=False)
+    qs = q[:, :, rows].float().cpu().double().numpy()
+    kk = k.float().cpu().double().numpy()
+    vv = v.float().cpu().double().numpy()
+    sc = np.einsum("bhid,bhjd->bhij", qs, kk) / math.sqrt(D)
+    if causal:
+        sc = np.where(np.arange(N)[None, None, None, :] <= rows[None, None, :, None], sc, -np.inf)
+    sc -= sc.max(-1, keepdims=True)
+    p = np.exp(sc)
+    p /= p.sum(-1, keepdims=True)
+    ref_o = np.einsum("bhij,bhjd->bhid", p, vv)
+    return float(np.abs(out[:, :, rows].float().cpu().double().numpy() - ref_o).max())
+
+
+# BASELINE config 2 (non-causal fp16 / fp32) and config 3 (causal fp16, with the non-divisible
+# lengths) at B1 H8 d64: (dtype, causal, seq_len)
+_CONFIG_CASES = ([("fp16", False, n) for n in (1024, 4096, 16384, 65536)]
+                 + [("fp32", False, n) for n in (1024, 4096, 16384, 65536)]
+                 + [("fp16", True, n) for n in (2048, 8192, 32768, 197, 1025, 4097)])
+
+
+def _baseline_configs(args, lib, dev, stream):
+    """The other shapes of BASELINE configs 2 and 3, each timed as the main line is.
+
+    Per case: the kernels' HIP-event averages (forward = Phase 1 + Phase 2, backward = the three
+    backward stages), the algorithmic TFLOP/s and fraction of the dtype's dense MFMA peak, the
+    wall-clock of the public training step (twopass_attention_train + autograd.grad, host work
+    included) and a sampled fp64 check of the forward.  Inputs q, k, v, dO ~ N(0,1), seed 1234."""
+    import torch
+
+    import elsa_amd
+
+    res = {}
+    for dts, causal, n in _CONFIG_CASES:
+        if (dts, causal, n) == (args.dtype, bool(args.causal), args.seq) and (args.batch, args.heads, args.dim) == (1, 8, 64):
+            continue  # the main line
+        dt = {"fp16": torch.float16, "fp32": torch.float32}[dts]
+        gen = torch.Generator().manual_seed(1234)
+        q, k, v, do = (torch.randn((1, 8, n, 64), generator=gen).to(dt).to(dev) for _ in range(4))
+        f_fwd = _flops_fwd(1, 8, n, 64, causal)
+        steps = max(2, min(args.config_steps, int(2e13 / f_fwd) if dts == "fp32" else args.config_steps))
+        kern_ms, plan, out = _kernel_ms(lib, stream, q, k, v, do, causal, None, steps)
+        qg, kg, vg = (t.detach().requires_grad_() for t in (q, k, v))
+
+        def step():
+            o = elsa_amd.twopass_attention_train(qg, kg, vg, is_causal=causal)
+            return torch.autograd.grad(o, (qg, kg, vg), do)
+
+        step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        step_ms = e0.elapsed_time(e1) / steps
+        fwd_ms = kern_ms["phase1_fold"] + kern_ms["phase2_merge"]
+        bwd_ms = kern_ms["bwd_preprocess"] + kern_ms["bwd_dq"] + kern_ms["bwd_dkdv"]
+        peak = PEAK_TFLOPS[dts]
+        key = f"{dts}_{'causal_' if causal else ''}n{n}"
+        res[key] = {
+            "seq_len": n, "dtype": dts, "causal": causal, "partitions": plan["partitions"],
+            "partition_len": plan["partition_len"], "steps": steps,
+            "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
+            "fwd_tflops": round(f_fwd / (fwd_ms * 1e-3) / 1e12, 1),
+            "bwd_tflops": round(2.5 * f_fwd / (bwd_ms * 1e-3) / 1e12, 1),
+            "fwd_frac_peak": round(f_fwd / (fwd_ms * 1e-3) / 1e12 / peak, 4),
+            "bwd_frac_peak": round(2.5 * f_fwd / (bwd_ms * 1e-3) / 1e12 / peak, 4),
+            "train_step_ms": round(step_ms, 4),
+            "max_abs_sampled_fwd": _sampled_max_abs(q, k, v, out, causal, nrows=8),
+        }
+        print(f"bench: config {key}: fwd {fwd_ms:.4f} ms, bwd {bwd_ms:.4f} ms, step {step_ms:.4f} ms",
+              file=sys.stderr, flush=True)
+        del q, k, v, do, qg, kg, vg, out
+        torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     args = _args()
     if args.summarize_pmc:
@@ -181,14 +326,10 @@ def main() -> int:
               "by batch x heads with no communication). Run with --gpus 1.", file=sys.stderr, flush=True)
         return 2
 
-    import numpy as np
     import torch
 
     import elsa_amd
     from elsa_amd import _lib
-    from elsa_amd.attention import forward_plan
-    from elsa_amd.attention_bwd import _attach_workspace, _bwd_args
-    from elsa_amd.attention import _BiasMeta, _make_fwd_args
 
     dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[args.dtype]
     dev = torch.device("cuda:0")
@@ -236,42 +377,7 @@ def main() -> int:
     # ---- per-kernel HIP-event timing through the C ABI, on the stream the kernels run on
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev)
-    sh = stream.cuda_stream
-    plan = forward_plan(q, is_causal=causal, block_n=args.block_n)
-    out = torch.empty_like(q)
-    rm = torch.empty((B * H, N), device=dev, dtype=torch.float32)
-    rz = torch.empty_like(rm)
-    fa = _make_fwd_args(q, k, v, out, rm, rz, _BiasMeta(None, 0, 0, 0, 0, False), is_causal=causal,
-                        summary_dtype=dt, partition_len=args.block_n, q_chunk=None, scale=1.0 / math.sqrt(D),
-                        exact_row_max=False)  # the training forward's state, as in the step above
-    ws_f = torch.empty(plan["workspace_bytes"], dtype=torch.uint8, device=dev)
-    fa.workspace, fa.workspace_bytes = ws_f.data_ptr(), plan["workspace_bytes"]
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    ba = _bwd_args(q, k, v, out, do, rm, rz, dq, dk, dv, _BiasMeta(None, 0, 0, 0, 0, False), is_causal=causal,
-                   scale=1.0 / math.sqrt(D))
-    ws_b = _attach_workspace(lib, ba, dev)
-    qc = plan["q_chunk"]
-    chunks = [(s, min(qc, N - s)) for s in range(0, N, qc)]
-
-    launches = {
-        "phase1_fold": lambda: [lib.elsa_phase1(ctypes.byref(fa), s, n, sh) for s, n in chunks],
-        "phase2_merge": lambda: [lib.elsa_phase2(ctypes.byref(fa), s, n, sh) for s, n in chunks],
-        "bwd_preprocess": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 0, sh)],
-        "bwd_dq": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 1, sh)],
-        "bwd_dkdv": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 2, sh)],
-    }
-    kern_ms = {}
-    for name, fn in launches.items():
-        for rc in fn():
-            _lib.check(rc, name)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(args.steps):
-            fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        kern_ms[name] = e0.elapsed_time(e1) / args.steps
+    kern_ms, plan, out = _kernel_ms(lib, stream, q, k, v, do, causal, args.block_n, args.steps)
     print("bench: kernels " + ", ".join(f"{k_}={v_:.3f}ms" for k_, v_ in kern_ms.items()), file=sys.stderr,
           flush=True)
 
@@ -283,18 +389,7 @@ def main() -> int:
     vs_sdpa = _vs_sdpa(args, q, k, v, do, causal) if args.dtype == "fp16" else None
 
     # ---- sampled parity check of this very run (closed form, fp64 on CPU)
-    rows = np.random.default_rng(0).choice(N, 16, replace=False)
-    qs = q[:, :, rows].float().cpu().double().numpy()
-    kk = k.float().cpu().double().numpy()
-    vv = v.float().cpu().double().numpy()
-    sc = np.einsum("bhid,bhjd->bhij", qs, kk) / math.sqrt(D)
-    if causal:
-        sc = np.where(np.arange(N)[None, None, None, :] <= rows[None, None, :, None], sc, -np.inf)
-    sc -= sc.max(-1, keepdims=True)
-    p = np.exp(sc)
-    p /= p.sum(-1, keepdims=True)
-    ref_o = np.einsum("bhij,bhjd->bhid", p, vv)
-    max_abs = float(np.abs(out[:, :, rows].float().cpu().double().numpy() - ref_o).max())
+    max_abs = _sampled_max_abs(q, k, v, out, causal)
 
     # ---- derived numbers
     f_fwd = _flops_fwd(B, H, N, D, causal)
@@ -404,6 +499,8 @@ def main() -> int:
         torch.add(src, 1.0, out=dst)
         torch.cuda.synchronize()
         result["copy_calibration_mib"] = args.copy_mib
+    if args.configs:
+        result["baseline_configs"] = _baseline_configs(args, lib, dev, stream)
     if args.cpu_baseline:
         result["cpu_baseline"] = _cpu_baseline(args, B, H, N, D, causal)
     print(json.dumps(result), flush=True)

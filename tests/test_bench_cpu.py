@@ -103,3 +103,32 @@ def test_cpu_baseline_times_baseline_config_1():
     assert math.isclose(res["gflops"], 4 * 8 * 1024 ** 2 * 64 / (res["ms"] * 1e-3) / 1e9, rel_tol=1e-3)
     ns = res["north_star_sample"]
     assert ns["value"] > 0 and "rows 0..63" in ns["sample"]
+
+
+def test_baseline_config_cases_cover_configs_2_and_3():
+    """baseline_configs covers BASELINE config 2 (non-causal fp16 and fp32 at 1K, 4K, 16K, 64K) and
+    config 3 (causal fp16 at 2K, 8K, 32K and the non-divisible 197, 1025, 4097)."""
+    cases = set(bench._CONFIG_CASES)
+    for dt in ("fp16", "fp32"):
+        for n in (1024, 4096, 16384, 65536):
+            assert (dt, False, n) in cases
+    for n in (2048, 8192, 32768, 197, 1025, 4097):
+        assert ("fp16", True, n) in cases
+    assert len(cases) == len(bench._CONFIG_CASES) == 14
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_sampled_max_abs_sees_one_wrong_row(causal):
+    """The sampled forward check of every bench line: zero on the exact output, and a change to one
+    sampled row shows up at its size."""
+    import torch
+
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn((1, 2, 40, 8), generator=g, dtype=torch.float64) for _ in range(3))
+    mask = torch.ones(40, 40, dtype=torch.bool).tril() if causal else None
+    out = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+    # the check reads the tensors through fp32, as it reads the kernels' fp16 / fp32 outputs
+    assert bench._sampled_max_abs(q, k, v, out, causal, nrows=40) < 1e-6
+    bad = out.clone()
+    bad[0, 1, 17, 3] += 0.25
+    assert abs(bench._sampled_max_abs(q, k, v, bad, causal, nrows=40) - 0.25) < 1e-6
