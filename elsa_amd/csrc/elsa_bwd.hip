@@ -464,29 +464,69 @@ void bwd_dkdv_kernel(const BwdParams p) {
 // 16-byte copies (double-buffered through registers) and transposed MFMA operands
 // (K^T for dq; Q^T, dO^T for dk/dv) come from the transposing LDS load.  RT (dq)
 // and KRT (dk/dv) are the 32-wide tiles per wave.
-template <typename T, int DP>
+template <typename T, int DP, bool SWIZZLE>
 struct HalfStage {
   static constexpr int ST = 64;       // rows (or keys) per LDS stage
-  static constexpr int KS = DP + 8;   // LDS row stride in elements
-  static constexpr int CPR = DP / 8;  // 16-byte chunks per row
+  // At DP = 64 the rows are unpadded (128 bytes) and the 16-byte chunk q of row r sits at chunk
+  // q ^ swz(r), swz(r) = 4 (m % 2) + m / 2 with m = (r / 2) % 8.  Both read patterns are then
+  // free of bank conflicts: the 16 lanes of a row-fragment read (one chunk of 16 rows) land on 16
+  // distinct 4-bank groups, since the 8 rows of one parity take 8 distinct swz values; the 32 lanes
+  // of a transposing read (rows r..r+3 for r a multiple of 4, 64 bytes each) land on disjoint
+  // groups, since rows r and r + 2 differ in bit 2 of swz.  With the padded 72-element stride the
+  // transposing reads conflicted 2-way on a quarter of the banks: 74 against 133 TB/s of LDS
+  // reads over the chip in a read-only loop, where the row-fragment reads ran at 120 TB/s either way.
+  // (kernels whose registers have room for the per-lane read addresses it costs: 20-30 VGPRs)
+  static constexpr bool SWZ = SWIZZLE && DP == 64;
+  static constexpr int KS = SWZ ? DP : DP + 8;  // LDS row stride in elements
+  static constexpr int CPR = DP / 8;            // 16-byte chunks per row
+  __device__ static inline int swz(int r) {
+    const int m = (r >> 1) & 7;
+    return ((m & 1) << 2) | (m >> 1);
+  }
+  // element offset of (row r, column col) of a stage tile; col / 8 is its chunk
+  __device__ static inline int off(int r, int col) {
+    if constexpr (SWZ) {
+      return r * KS + ((((col >> 3) ^ swz(r)) << 3) | (col & 7));
+    } else {
+      return r * KS + col;
+    }
+  }
 };
 
+// the same from the lane's two element offsets, of rows r0..r0+3 and r0+4..r0+7
 template <typename T>
-__device__ inline typename Mfma<T>::frag tr_frag(const T* tile_row0, int ks, int col) {
-  // 8 consecutive rows (k) at column `col` of this lane: two transposing reads of 4 rows
-  const i16x4 lo = lds_read_tr16(tile_row0 + col);
-  const i16x4 hi = lds_read_tr16(tile_row0 + 4 * ks + col);
+__device__ inline typename Mfma<T>::frag tr_frag_off(const T* base, int o0, int o1) {
+  const i16x4 lo = lds_read_tr16(base + o0);
+  const i16x4 hi = lds_read_tr16(base + o1);
   const i16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return __builtin_bit_cast(typename Mfma<T>::frag, both);
 }
+
+// 8 consecutive rows (k) r0..r0+7 of a HalfStage tile at column `col` of this lane: two
+// transposing reads of 4 rows
+template <typename T, typename Tile>
+__device__ inline typename Mfma<T>::frag tr_frag_at(const T* tile, int r0, int col) {
+  i16x4 lo, hi;
+  if constexpr (Tile::SWZ) {
+    lo = lds_read_tr16(tile + Tile::off(r0, col));
+    hi = lds_read_tr16(tile + Tile::off(r0 + 4, col));
+  } else {
+    const T* row0 = tile + r0 * Tile::KS;
+    lo = lds_read_tr16(row0 + col);
+    hi = lds_read_tr16(row0 + 4 * Tile::KS + col);
+  }
+  const i16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(typename Mfma<T>::frag, both);
+}
+
 
 template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void bwd_dq_half_kernel(const BwdParams p) {
   using M = Mfma<T>;
   typedef typename M::frag F;
-  using S = HalfStage<T, DP>;
-  constexpr int KT = S::ST, KS = S::KS, CPR = S::CPR;
+  using Tile = HalfStage<T, DP, false>;
+  constexpr int KT = Tile::ST, KS = Tile::KS, CPR = Tile::CPR;
   constexpr int NKK = DP / 16, NDT = DP / 32;
   constexpr int NT = 64 * WAVES, ROWS_W = 32 * RT, BM = ROWS_W * WAVES;
   static_assert((KT * CPR) % NT == 0, "staging must divide evenly");
@@ -511,6 +551,16 @@ void bwd_dq_half_kernel(const BwdParams p) {
   const T* dO = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1];
   const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  // swizzled tiles: this lane's offsets within a 32-key sub-tile (as in bwd_dkdv_half_kernel)
+  int o_row[Tile::SWZ ? NKK : 1], o_tr[Tile::SWZ ? NDT : 1][2];
+  if constexpr (Tile::SWZ) {
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) o_row[kk] = Tile::off(swap23(c), g * 8 + kk * 16);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) o_tr[dt][h] = Tile::off(tr_row + 4 * h, dt * 32 + tr_col);
+  }
 
   F qf[RT][NKK], gf[RT][NKK];
   float lse[RT], dd[RT];
@@ -578,8 +628,9 @@ static_for<0, NCH>([&](auto I) {
       constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
-      *reinterpret_cast<Chunk16*>(&Ks[buf][r * KS + d0]) = kreg[S][i];
-      *reinterpret_cast<Chunk16*>(&Vs[buf][r * KS + d0]) = vreg[S][i];
+      const int lo = Tile::SWZ ? Tile::off(r, d0) : r * KS + d0;
+      *reinterpret_cast<Chunk16*>(&Ks[buf][lo]) = kreg[S][i];
+      *reinterpret_cast<Chunk16*>(&Vs[buf][lo]) = vreg[S][i];
     });
   };
 
@@ -598,12 +649,20 @@ static_for<0, NCH>([&](auto I) {
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         F kf[NKK], vf[NKK];
-        const T* krow = ks + (sub * 32 + swap23(c)) * KS + g * 8;
-        const T* vrow = vs + (sub * 32 + swap23(c)) * KS + g * 8;
+        if constexpr (Tile::SWZ) {
 #pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) {
-          kf[kk] = *reinterpret_cast<const F*>(krow + kk * 16);
-          vf[kk] = *reinterpret_cast<const F*>(vrow + kk * 16);
+          for (int kk = 0; kk < NKK; ++kk) {
+            kf[kk] = *reinterpret_cast<const F*>(ks + sub * 32 * KS + o_row[kk]);
+            vf[kk] = *reinterpret_cast<const F*>(vs + sub * 32 * KS + o_row[kk]);
+          }
+        } else {
+          const T* krow = ks + (sub * 32 + swap23(c)) * KS + g * 8;
+          const T* vrow = vs + (sub * 32 + swap23(c)) * KS + g * 8;
+#pragma unroll
+          for (int kk = 0; kk < NKK; ++kk) {
+            kf[kk] = *reinterpret_cast<const F*>(krow + kk * 16);
+            vf[kk] = *reinterpret_cast<const F*>(vrow + kk * 16);
+          }
         }
         F dsp[RT][2];  // dS of the sub-tile, rounded to T: the B operand of the dQ^T product
 #pragma unroll
@@ -650,7 +709,13 @@ static_for<0, NCH>([&](auto I) {
         for (int j = 0; j < 2; ++j) {
           F ka[NDT];
 #pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) ka[dt] = tr_frag<T>(ks + (sub * 32 + 16 * j + tr_row) * KS, KS, dt * 32 + tr_col);
+          for (int dt = 0; dt < NDT; ++dt) {
+            if constexpr (Tile::SWZ) {
+              ka[dt] = tr_frag_off<T>(ks + (sub * 32 + 16 * j) * KS, o_tr[dt][0], o_tr[dt][1]);
+            } else {
+              ka[dt] = tr_frag_at<T, Tile>(ks, sub * 32 + 16 * j + tr_row, dt * 32 + tr_col);
+            }
+          }
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -735,8 +800,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(DP >
 void bwd_dkdv_half_kernel(const BwdParams p) {
   using M = Mfma<T>;
   typedef typename M::frag F;
-  using S = HalfStage<T, DP>;
-  constexpr int RTS = S::ST, KS = S::KS, CPR = S::CPR;  // rows per stage
+  // swizzled tiles in the 8-wave kernel: 16K d64 1.093 -> 1.081 ms (fp16), 1.045 -> 1.028 ms (bf16),
+  // causal 0.574 -> 0.564 ms; the 4-wave one has no registers for it
+  using Tile = HalfStage<T, DP, true>;
+  constexpr int RTS = Tile::ST, KS = Tile::KS, CPR = Tile::CPR;  // rows per stage
   constexpr int NKK = DP / 16, NDT = DP / 32;
   constexpr int NT = 64 * WAVES, KEYS_W = 32 * KRT, BN = KEYS_W * WAVES;
   static_assert((RTS * CPR) % NT == 0, "staging must divide evenly");
@@ -759,6 +826,18 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
   const T* dO = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1];
   const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  // swizzled tiles: this lane's element offsets within a 32-row sub-tile, for its row fragments
+  // (row swap23(c), chunk g + 2 kk) and its transposing reads (rows tr_row + 4h, column
+  // 32 dt + tr_col); the swizzle reads bits 1-3 of a row only, so they hold in every sub-tile
+  int o_row[Tile::SWZ ? NKK : 1], o_tr[Tile::SWZ ? NDT : 1][2];
+  if constexpr (Tile::SWZ) {
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) o_row[kk] = Tile::off(swap23(c), g * 8 + kk * 16);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) o_tr[dt][h] = Tile::off(tr_row + 4 * h, dt * 32 + tr_col);
+  }
 
   F kf[KRT][NKK], vf[KRT][NKK];
   bool key_ok[KRT];
@@ -824,8 +903,9 @@ static_for<0, NCH>([&](auto I) {
       constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
-      *reinterpret_cast<Chunk16*>(&Qs[buf][r * KS + d0]) = qreg[S][i];
-      *reinterpret_cast<Chunk16*>(&Gs[buf][r * KS + d0]) = greg[S][i];
+      const int lo = Tile::SWZ ? Tile::off(r, d0) : r * KS + d0;
+      *reinterpret_cast<Chunk16*>(&Qs[buf][lo]) = qreg[S][i];
+      *reinterpret_cast<Chunk16*>(&Gs[buf][lo]) = greg[S][i];
     });
     if (tid < RTS) {
       lse_s[buf][tid] = lreg[S];
@@ -847,12 +927,20 @@ static_for<0, NCH>([&](auto I) {
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         F qa[NKK], ga[NKK];
-        const T* qrow = qs + (sub * 32 + swap23(c)) * KS + g * 8;
-        const T* grow = gs + (sub * 32 + swap23(c)) * KS + g * 8;
+        if constexpr (Tile::SWZ) {
 #pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) {
-          qa[kk] = *reinterpret_cast<const F*>(qrow + kk * 16);
-          ga[kk] = *reinterpret_cast<const F*>(grow + kk * 16);
+          for (int kk = 0; kk < NKK; ++kk) {
+            qa[kk] = *reinterpret_cast<const F*>(qs + sub * 32 * KS + o_row[kk]);
+            ga[kk] = *reinterpret_cast<const F*>(gs + sub * 32 * KS + o_row[kk]);
+          }
+        } else {
+          const T* qrow = qs + (sub * 32 + swap23(c)) * KS + g * 8;
+          const T* grow = gs + (sub * 32 + swap23(c)) * KS + g * 8;
+#pragma unroll
+          for (int kk = 0; kk < NKK; ++kk) {
+            qa[kk] = *reinterpret_cast<const F*>(qrow + kk * 16);
+            ga[kk] = *reinterpret_cast<const F*>(grow + kk * 16);
+          }
         }
         // transposed Q^T / dO^T fragments for the dK / dV products, shared by the KRT key tiles
         F gta[2][NDT], qta[2][NDT];
@@ -860,8 +948,13 @@ static_for<0, NCH>([&](auto I) {
         for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) {
-            gta[j][dt] = tr_frag<T>(gs + (sub * 32 + 16 * j + tr_row) * KS, KS, dt * 32 + tr_col);
-            qta[j][dt] = tr_frag<T>(qs + (sub * 32 + 16 * j + tr_row) * KS, KS, dt * 32 + tr_col);
+            if constexpr (Tile::SWZ) {
+              gta[j][dt] = tr_frag_off<T>(gs + (sub * 32 + 16 * j) * KS, o_tr[dt][0], o_tr[dt][1]);
+              qta[j][dt] = tr_frag_off<T>(qs + (sub * 32 + 16 * j) * KS, o_tr[dt][0], o_tr[dt][1]);
+            } else {
+              gta[j][dt] = tr_frag_at<T, Tile>(gs, sub * 32 + 16 * j + tr_row, dt * 32 + tr_col);
+              qta[j][dt] = tr_frag_at<T, Tile>(qs, sub * 32 + 16 * j + tr_row, dt * 32 + tr_col);
+            }
           }
         // -D of the rows of registers 8j..8j+7 (sub*32 + 16j + 8g + t): the dP^T product starts
         // from it and yields dP - D directly
