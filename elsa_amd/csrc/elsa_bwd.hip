@@ -467,33 +467,25 @@ void bwd_dkdv_kernel(const BwdParams p) {
 template <typename T, int DP, bool SWIZZLE>
 struct HalfStage {
   static constexpr int ST = 64;       // rows (or keys) per LDS stage
-  // At DP = 64 the rows are unpadded (128 bytes) and the 16-byte chunk q of row r sits at chunk
-  // q ^ swz(r), swz(r) = 4 (m % 2) + m / 2 with m = (r / 2) % 8.  Both read patterns are then
-  // free of bank conflicts: the 16 lanes of a row-fragment read (one chunk of 16 rows) land on 16
-  // distinct 4-bank groups, since the 8 rows of one parity take 8 distinct swz values; the 32 lanes
-  // of a transposing read (rows r..r+3 for r a multiple of 4, 64 bytes each) land on disjoint
-  // groups, since rows r and r + 2 differ in bit 2 of swz.  With the padded 72-element stride the
-  // transposing reads conflicted 2-way on a quarter of the banks: 74 against 133 TB/s of LDS
-  // reads over the chip in a read-only loop, where the row-fragment reads ran at 120 TB/s either way.
-  // (kernels whose registers have room for the per-lane read addresses it costs: 20-30 VGPRs)
+  // At DP = 64 and SWIZZLE: unpadded rows with XOR-swizzled chunks (lds_swz_off).  Over the
+  // whole chip in a read-only loop, the transposing reads of padded 72-element rows ran at 74
+  // against 133 TB/s of LDS reads swizzled (they conflicted 2-way on a quarter of the banks), the
+  // row fragments at 119-120 TB/s either way.
   static constexpr bool SWZ = SWIZZLE && DP == 64;
   static constexpr int KS = SWZ ? DP : DP + 8;  // LDS row stride in elements
   static constexpr int CPR = DP / 8;            // 16-byte chunks per row
-  __device__ static inline int swz(int r) {
-    const int m = (r >> 1) & 7;
-    return ((m & 1) << 2) | (m >> 1);
-  }
   // element offset of (row r, column col) of a stage tile; col / 8 is its chunk
   __device__ static inline int off(int r, int col) {
     if constexpr (SWZ) {
-      return r * KS + ((((col >> 3) ^ swz(r)) << 3) | (col & 7));
+      return lds_swz_off(r, col);
     } else {
       return r * KS + col;
     }
   }
 };
 
-// the same from the lane's two element offsets, of rows r0..r0+3 and r0+4..r0+7
+// 8 consecutive rows of a column: two transposing reads at this lane's element offsets o0 (rows
+// r0..r0+3) and o1 (rows r0+4..r0+7)
 template <typename T>
 __device__ inline typename Mfma<T>::frag tr_frag_off(const T* base, int o0, int o1) {
   const i16x4 lo = lds_read_tr16(base + o0);

@@ -150,6 +150,20 @@ __device__ inline float sum2(bf16 a, bf16 b, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(v, one, acc, false);
 }
 
+// Unpadded LDS tiles of 64 two-byte elements per row (128 bytes) with the 16-byte chunk q of row r
+// stored at chunk q ^ lds_swz(r), lds_swz(r) = 4 (m % 2) + m / 2 with m = (r / 2) % 8.  Both
+// fragment reads of the kernels are then free of bank conflicts: the 16 lanes of a row-fragment
+// read (one chunk of 16 rows) land on 16 distinct 4-bank groups, since the 8 rows of one parity
+// take 8 distinct lds_swz values; the 32 lanes of a transposing read (rows r..r+3 for r a multiple
+// of 4, 64 bytes each) land on disjoint groups, since rows r and r + 2 differ in bit 2 of lds_swz.
+// No padded stride serves both: the row fragments need an odd multiple of 4 banks, the
+// transposing reads 16 or 48.  lds_swz reads bits 1-3 of the row only, so offsets computed
+// for one 16-row block hold in every other.
+__device__ __host__ constexpr inline int lds_swz(int r) { return (((r >> 1) & 1) << 2) | ((r >> 2) & 3); }
+__device__ __host__ constexpr inline int lds_swz_off(int r, int col) {
+  return r * 64 + ((((col >> 3) ^ lds_swz(r)) << 3) | (col & 7));
+}
+
 // Transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane group, source
 // lane s = 4t + a reads 4 16-bit elements at its own address; result lane
 // i = 4a' + b' receives element b' of source lanes a' + 4t, t = 0..3.  Pointing
