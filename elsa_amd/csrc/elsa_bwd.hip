@@ -795,7 +795,9 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
   // swizzled tiles in the 8-wave kernel: 16K d64 1.093 -> 1.081 ms (fp16), 1.045 -> 1.028 ms (bf16),
   // causal 0.574 -> 0.564 ms; the 4-wave one has no registers for it
   using Tile = HalfStage<T, DP, true>;
-  constexpr int RTS = Tile::ST, KS = Tile::KS, CPR = Tile::CPR;  // rows per stage
+  // rows per stage: 128 in the 8-wave kernel, so that one barrier serves twice the rows (16K d64 dK/dV
+  // 1.056 -> 1.042 ms fp16, 1.005 -> 0.992 ms bf16, causal 0.556 -> 0.551 ms; 256 VGPRs, no spill)
+  constexpr int RTS = WAVES == 8 ? 128 : Tile::ST, KS = Tile::KS, CPR = Tile::CPR;
   constexpr int NKK = DP / 16, NDT = DP / 32;
   constexpr int NT = 64 * WAVES, KEYS_W = 32 * KRT, BN = KEYS_W * WAVES;
   static_assert((RTS * CPR) % NT == 0, "staging must divide evenly");
@@ -855,14 +857,14 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
     }
 
   // element offsets of this thread's staging chunks inside a stage (row strides are
-  // below 2^25 elements, checked by the API, so 64 rows fit in 32 bits)
-  int32_t qoff[NCH], goff[NCH];
+  // below 2^25 elements, checked by the API, so the 128 rows of a stage fit in 32 unsigned bits)
+  uint32_t qoff[NCH], goff[NCH];
   static_for<0, NCH>([&](auto I) {
     constexpr int i = decltype(I)::value;
     const int ci = tid + i * NT;
     const int r = ci / CPR, d0 = (ci % CPR) * 8;
-    qoff[i] = r * (int32_t)p.qs[2] + d0;
-    goff[i] = r * (int32_t)p.gs[2] + d0;
+    qoff[i] = (uint32_t)r * (uint32_t)p.qs[2] + (uint32_t)d0;
+    goff[i] = (uint32_t)r * (uint32_t)p.gs[2] + (uint32_t)d0;
   });
   // staging registers: set S holds one 64-row stage on its way from global memory to LDS
   Chunk16 qreg[2][NCH], greg[2][NCH];
@@ -917,7 +919,7 @@ static_for<0, NCH>([&](auto I) {
       const T* qs = Qs[buf];
       const T* gs = Gs[buf];
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
+      for (int sub = 0; sub < RTS / 32; ++sub) {
         F qa[NKK], ga[NKK];
         if constexpr (Tile::SWZ) {
 #pragma unroll
