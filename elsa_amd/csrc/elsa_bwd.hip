@@ -866,7 +866,7 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
     qoff[i] = (uint32_t)r * (uint32_t)p.qs[2] + (uint32_t)d0;
     goff[i] = (uint32_t)r * (uint32_t)p.gs[2] + (uint32_t)d0;
   });
-  // staging registers: set S holds one 64-row stage on its way from global memory to LDS
+  // staging registers: set S holds one stage (RTS rows) on its way from global memory to LDS
   Chunk16 qreg[2][NCH], greg[2][NCH];
   float lreg[2] = {0.f, 0.f}, dreg[2] = {0.f, 0.f};
   auto gload = [&](int t0, auto SET) {
