@@ -1397,16 +1397,26 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
       }
     }
     if (stage < 0 || stage == 1) {
-      // dq with two 32-row tiles per wave (256-row work-groups): each K/V fragment read from LDS
-      // feeds both tiles, halving the LDS reads per MFMA.  Non-causal, unbiased, D <= 64, and only
-      // where the grid still puts two work-groups on every CU.  B1 H8 d64 16K: fp16 0.875 -> 0.814
-      // ms, bf16 0.841 -> 0.768 ms; causal 16K 0.479 against 0.510 ms and 4K (128 work-groups)
-      // 0.074 against 0.111 ms stay on the 32-row kernel.
+      // dq with two 32-row tiles per wave: each K/V fragment read from LDS feeds both tiles,
+      // halving the LDS reads per MFMA.  Non-causal, unbiased, D <= 64, and only where the grid
+      // still puts two 256-row work-groups on every CU.  B1 H8 d64 16K: fp16 0.875 -> 0.814 ms, bf16
+      // 0.841 -> 0.768 ms; causal 16K 0.479 against 0.510 ms and 4K (128 work-groups) 0.074 against
+      // 0.111 ms stay on the 32-row kernel.  At D = 64, 8-wave work-groups of 512 rows (one per CU,
+      // 246 VGPRs), so each K/V stage staged once serves twice the rows: 16K 0.794 -> 0.766 ms (fp16),
+      // 0.750 -> 0.720 ms (bf16), B2 H8 8K 0.404 -> 0.388 ms, 64K 12.13 -> 11.86 ms.
       const dim3 grid2((p.N + 255) / 256, p.BH);
       bool wide = false;
       if constexpr (DP <= 64 && !B) {
         wide = !p.causal && (int64_t)grid2.x * grid2.y >= 512;
-        if (wide) hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, 2, W, false>), grid2, dim3(64 * W), 0, st, p);
+        bool w8 = false;
+        if constexpr (DP == 64) {
+          const dim3 grid8((p.N + 511) / 512, p.BH);
+          if (wide && (int64_t)grid8.x * grid8.y >= 256) {
+            hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, 2, 8, false>), grid8, dim3(512), 0, st, p);
+            w8 = true;
+          }
+        }
+        if (wide && !w8) hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, 2, W, false>), grid2, dim3(64 * W), 0, st, p);
       }
       // otherwise, at D = 64 with the same grid condition, 8-wave work-groups of 32-row tiles
       // (256 rows): the K/V stage staged once for twice the rows.  Causal 16K dq 0.466 -> 0.412 ms,

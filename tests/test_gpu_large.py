@@ -135,7 +135,8 @@ FULL = [
     ((8, 3, 2305, 64), "fp16", False),
     ((1, 8, 2048, 64), "fp16", True),    # causal config: N=2048 forward and backward
     ((1, 8, 4097, 64), "fp16", True),    # causal NEEDS_MASK length
-    ((4, 32, 1024, 64), "fp16", False),  # 512 dq work-groups of 256 rows: the two-tile dq kernel
+    ((4, 32, 1024, 64), "fp16", False),  # the two-tile dq kernel in 256 8-wave work-groups of 512 rows
+    ((2, 16, 4160, 64), "bf16", False),  # the same with a partial last work-group (64 of its 512 rows)
     ((2, 64, 1024, 64), "bf16", False),
     ((4, 32, 1024, 64), "fp16", True),   # causal: the 8-wave dq and dK/dV work-groups
     ((1, 8, 2048, 64), "bf16", False),   # the split backward (four key / row ranges, fp32 partials)
