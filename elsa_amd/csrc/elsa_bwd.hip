@@ -466,7 +466,7 @@ void bwd_dkdv_kernel(const BwdParams p) {
 // and KRT (dk/dv) are the 32-wide tiles per wave.
 template <typename T, int DP, bool SWIZZLE>
 struct HalfStage {
-  static constexpr int ST = 64;       // rows (or keys) per LDS stage
+  static constexpr int ST = 64;       // rows (or keys) per LDS stage (the 8-wave dK/dV kernel: 128)
   // At DP = 64 and SWIZZLE: unpadded rows with XOR-swizzled chunks (lds_swz_off).  Over the
   // whole chip in a read-only loop, the transposing reads of padded 72-element rows ran at 74
   // against 133 TB/s of LDS reads swizzled (they conflicted 2-way on a quarter of the banks), the
