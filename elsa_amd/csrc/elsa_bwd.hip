@@ -498,15 +498,10 @@ __device__ inline typename Mfma<T>::frag tr_frag_off(const T* base, int o0, int 
 // transposing reads of 4 rows
 template <typename T, typename Tile>
 __device__ inline typename Mfma<T>::frag tr_frag_at(const T* tile, int r0, int col) {
-  i16x4 lo, hi;
-  if constexpr (Tile::SWZ) {
-    lo = lds_read_tr16(tile + Tile::off(r0, col));
-    hi = lds_read_tr16(tile + Tile::off(r0 + 4, col));
-  } else {
-    const T* row0 = tile + r0 * Tile::KS;
-    lo = lds_read_tr16(row0 + col);
-    hi = lds_read_tr16(row0 + 4 * Tile::KS + col);
-  }
+  static_assert(!Tile::SWZ, "padded rows (swizzled tiles read through tr_frag_off)");
+  const T* row0 = tile + r0 * Tile::KS;
+  const i16x4 lo = lds_read_tr16(row0 + col);
+  const i16x4 hi = lds_read_tr16(row0 + 4 * Tile::KS + col);
   const i16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return __builtin_bit_cast(typename Mfma<T>::frag, both);
 }
@@ -517,6 +512,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 void bwd_dq_half_kernel(const BwdParams p) {
   using M = Mfma<T>;
   typedef typename M::frag F;
+  // padded rows: with the swizzled tiles of bwd_dkdv_half_kernel the one-tile dq measured 1-2% slower,
+  // and the two-tile one has no registers for the lane offsets
   using Tile = HalfStage<T, DP, false>;
   constexpr int KT = Tile::ST, KS = Tile::KS, CPR = Tile::CPR;
   constexpr int NKK = DP / 16, NDT = DP / 32;
@@ -543,16 +540,6 @@ void bwd_dq_half_kernel(const BwdParams p) {
   const T* dO = static_cast<const T*>(p.dout) + bi * p.gs[0] + hi * p.gs[1];
   const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  // swizzled tiles: this lane's offsets within a 32-key sub-tile (as in bwd_dkdv_half_kernel)
-  int o_row[Tile::SWZ ? NKK : 1], o_tr[Tile::SWZ ? NDT : 1][2];
-  if constexpr (Tile::SWZ) {
-#pragma unroll
-    for (int kk = 0; kk < NKK; ++kk) o_row[kk] = Tile::off(swap23(c), g * 8 + kk * 16);
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) o_tr[dt][h] = Tile::off(tr_row + 4 * h, dt * 32 + tr_col);
-  }
 
   F qf[RT][NKK], gf[RT][NKK];
   float lse[RT], dd[RT];
@@ -620,9 +607,8 @@ static_for<0, NCH>([&](auto I) {
       constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
       const int r = ci / CPR, d0 = (ci % CPR) * 8;
-      const int lo = Tile::SWZ ? Tile::off(r, d0) : r * KS + d0;
-      *reinterpret_cast<Chunk16*>(&Ks[buf][lo]) = kreg[S][i];
-      *reinterpret_cast<Chunk16*>(&Vs[buf][lo]) = vreg[S][i];
+      *reinterpret_cast<Chunk16*>(&Ks[buf][r * KS + d0]) = kreg[S][i];
+      *reinterpret_cast<Chunk16*>(&Vs[buf][r * KS + d0]) = vreg[S][i];
     });
   };
 
@@ -641,20 +627,12 @@ static_for<0, NCH>([&](auto I) {
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         F kf[NKK], vf[NKK];
-        if constexpr (Tile::SWZ) {
+        const T* krow = ks + (sub * 32 + swap23(c)) * KS + g * 8;
+        const T* vrow = vs + (sub * 32 + swap23(c)) * KS + g * 8;
 #pragma unroll
-          for (int kk = 0; kk < NKK; ++kk) {
-            kf[kk] = *reinterpret_cast<const F*>(ks + sub * 32 * KS + o_row[kk]);
-            vf[kk] = *reinterpret_cast<const F*>(vs + sub * 32 * KS + o_row[kk]);
-          }
-        } else {
-          const T* krow = ks + (sub * 32 + swap23(c)) * KS + g * 8;
-          const T* vrow = vs + (sub * 32 + swap23(c)) * KS + g * 8;
-#pragma unroll
-          for (int kk = 0; kk < NKK; ++kk) {
-            kf[kk] = *reinterpret_cast<const F*>(krow + kk * 16);
-            vf[kk] = *reinterpret_cast<const F*>(vrow + kk * 16);
-          }
+        for (int kk = 0; kk < NKK; ++kk) {
+          kf[kk] = *reinterpret_cast<const F*>(krow + kk * 16);
+          vf[kk] = *reinterpret_cast<const F*>(vrow + kk * 16);
         }
         F dsp[RT][2];  // dS of the sub-tile, rounded to T: the B operand of the dQ^T product
 #pragma unroll
@@ -701,13 +679,7 @@ static_for<0, NCH>([&](auto I) {
         for (int j = 0; j < 2; ++j) {
           F ka[NDT];
 #pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) {
-            if constexpr (Tile::SWZ) {
-              ka[dt] = tr_frag_off<T>(ks + (sub * 32 + 16 * j) * KS, o_tr[dt][0], o_tr[dt][1]);
-            } else {
-              ka[dt] = tr_frag_at<T, Tile>(ks, sub * 32 + 16 * j + tr_row, dt * 32 + tr_col);
-            }
-          }
+          for (int dt = 0; dt < NDT; ++dt) ka[dt] = tr_frag_at<T, Tile>(ks, sub * 32 + 16 * j + tr_row, dt * 32 + tr_col);
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
