@@ -397,12 +397,18 @@ __global__ __launch_bounds__(64 * WAVES) void phase1_kernel(const Phase1Params p
 constexpr float kLazyTau = 8.0f;
 constexpr float kLazySum = 256.0f;  // 2^kLazyTau
 
+// PV32 (fp16 inputs with fp32 summaries): the P.V product takes p unrounded, as the reference's
+// summary kernel does under SUMMARY_DOT_FP32 (attention_parallel_scan.py:701, :902;
+// attention.py:96-99).  p is split into p_hi = fp16(p) and p_lo = fp16(p - p_hi), and both halves
+// go through the fp16 MFMA (exact products, fp32 sums): p is carried to about 22 bits.
+//
 // 2 waves per SIMD, except the 1- and 2-wave variants at D >= 64 (sequences of at most 64
 // keys): their register staging of a whole 64-key stage does not fit that budget.
-template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS, bool PRE>
+template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS, bool PRE, bool PV32 = false>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu((WAVES <= 2 && DP >= 64) ? 1 : 2, 2)))
 void phase1_half_kernel(const Phase1Params p) {
   static_assert(!(PRE && HAS_BIAS), "the prescaled fold has no bias");
+  static_assert(!PV32 || (std::is_same<T, f16>::value && !PRE), "PV32 is the fp16 fold with fp32 summaries");
   using M = Mfma<T>;
   typedef typename M::frag F;
   constexpr int KT = 64;          // keys per LDS stage
@@ -662,6 +668,13 @@ void phase1_half_kernel(const Phase1Params p) {
             for (int t = 0; t < 8; ++t) b[t] = static_cast<T>(s[rt][sub][j * 8 + t]);
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) oacc[rt][dt] = M::mma(va[dt], b, oacc[rt][dt]);
+            if constexpr (PV32) {
+              F lo;
+#pragma unroll
+              for (int t = 0; t < 8; ++t) lo[t] = static_cast<T>(s[rt][sub][j * 8 + t] - static_cast<float>(b[t]));
+#pragma unroll
+              for (int dt = 0; dt < NDT; ++dt) oacc[rt][dt] = M::mma(va[dt], lo, oacc[rt][dt]);
+            }
           }
         }
     }
@@ -1259,7 +1272,8 @@ static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
     // 64K 8.59 -> 8.13 ms, 8K 0.181 -> 0.175 ms; at 4K (256-key partitions) 0.054 against
     // 0.061 ms.  Both kernels give the same bits, so the choice never changes a result.
     const dim3 g2((p.q_len + 511) / 512, p.BH, p.P);
-    if (!p.causal && p.part_len >= 1024) {
+    const bool pv32 = std::is_same<T, f16>::value && p.s_dtype == ELSA_F32;
+    if (!p.causal && p.part_len >= 1024 && !pv32) {
       bool done = false;
       if constexpr (std::is_same<T, f16>::value) {
         if (p.prescale_q) {
@@ -1284,6 +1298,12 @@ static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
   if constexpr (!B && DP == 64 && std::is_same<T, f16>::value) {
     if (p.prescale_q) {
       hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, false, true>), grid, dim3(64 * W), 0, st, p);
+      return hipGetLastError();
+    }
+  }
+  if constexpr (std::is_same<T, f16>::value) {
+    if (p.s_dtype == ELSA_F32) {  // p unrounded for P.V (the ping-pong fold has no such variant)
+      hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, B, false, true>), grid, dim3(64 * W), 0, st, p);
       return hipGetLastError();
     }
   }

@@ -294,6 +294,7 @@ def phase1_partition(
     mode: str,
     micro: int = 64,
     generic: Optional[bool] = None,
+    summary_dtype: Optional[str] = None,
 ):
     """Fold one K partition ``[k_begin, k_end)`` into a running (m, z, s) summary.
 
@@ -315,8 +316,11 @@ def phase1_partition(
     m_run = np.full((bh, r), NEG_INF, dtype=wd)
     z_run = np.zeros((bh, r), dtype=wd)
     s_run = np.zeros((bh, r, d), dtype=wd)
-    # p @ v in fp32 for the generic non-fp16 kernels (SUMMARY_DOT_FP32, attention.py:96-99)
-    p_round = mode != "fp64" and (dtype == "fp16")
+    # p @ v takes p rounded to fp16 only for fp16 inputs with 16-bit summaries: the reference
+    # launches its summary kernel with SUMMARY_DOT_FP32 = q.dtype != fp16 or summary_dtype ==
+    # fp32 (attention_parallel_scan.py:701, :902) and then forms p @ v from the fp32 p
+    # (attention.py:96-99); its fp16 d64 folds cast p to fp16 (attention_parallel_scan.py:167, :283)
+    p_round = mode != "fp64" and dtype == "fp16" and (summary_dtype or dtype) != "fp32"
     for t0 in range(k_begin, k_end, micro):
         t1 = min(t0 + micro, k_end)
         kt = k[:, t0:t1]
@@ -403,6 +407,7 @@ def forward(
         m, z, s = phase1_partition(
             qf[:, rows], kf, vf, row_idx=rows, k_begin=k0, k_end=min(n, k0 + part_len), n_ctx=n,
             is_causal=is_causal, bias=bb, dtype=dtype, mode=mode, micro=micro, generic=generic,
+            summary_dtype=summary_dtype,
         )
         parts.append((m, z, _summary_round(s, summary_dtype, mode)))
     if merge_kind == "tree":

@@ -181,7 +181,9 @@ def forward(q, k, v, *, bias=None, is_causal: bool = False, part_len: Optional[i
     if mode == "fp64":
         generic = True
     scale = 1.0 / math.sqrt(d)
-    p_round = mode != "fp64" and dtype == "fp16"
+    # p rounded to fp16 for p @ v only without SUMMARY_DOT_FP32 (fp16 inputs, 16-bit summaries:
+    # attention_parallel_scan.py:701, :902; attention.py:96-99)
+    p_round = mode != "fp64" and dtype == "fp16" and summary_dtype != "fp32"
     part_len = part_len or n
     outs, ms, zs = [], [], []
     for r0 in range(0, len(rows_t), row_chunk):

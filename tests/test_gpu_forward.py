@@ -155,6 +155,36 @@ def test_summary_dtypes_agree():
         assert max_abs(host(out), eo) <= (3e-3 if sd == torch.bfloat16 else 1e-3)
 
 
+# fp16 inputs with summary_dtype=fp32: the reference's summary kernel runs with SUMMARY_DOT_FP32
+# (attention_parallel_scan.py:701, :902) and forms p @ v from the fp32 p (attention.py:96-99);
+# the fold keeps p to ~22 bits there (a hi/lo fp16 split of p), so the plain bar applies.
+F32SUM = [
+    ((1, 2, 1025, 64), False, 256),
+    ((1, 2, 1025, 64), True, 256),
+    ((1, 3, 4096, 64), False, None),   # planner routing (1024-key partitions, the 4-wave fold)
+    ((2, 2, 300, 32), False, 128),
+]
+
+
+@pytest.mark.parametrize("case", F32SUM, ids=[f"{c[0]}-{'causal' if c[1] else 'full'}-bn{c[2]}" for c in F32SUM])
+def test_fp16_inputs_with_fp32_summaries(case):
+    shape, causal, bn = case
+    describe(f"fp16 inputs, fp32 summaries {shape} causal={causal} block_n={bn}")
+    q, k, v = O.make_inputs(shape, seed=21, dtype="fp16")
+    plan = forward_plan(dev(q, "fp16"), is_causal=causal, block_n=bn, summary_dtype=torch.float32)
+    assert plan["partitions"] >= 2, plan
+    out = elsa_amd.twopass_attention(dev(q, "fp16"), dev(k, "fp16"), dev(v, "fp16"), is_causal=causal, block_n=bn,
+                                     summary_dtype=torch.float32)
+    eo, _, _ = O.exact_forward(np.float32(q), np.float32(k), np.float32(v), is_causal=causal)
+    part = plan["partition_len"]
+    ro, _, _ = O.forward(q, k, v, is_causal=causal, part_len=part, dtype="fp16", mode="ref", summary_dtype="fp32")
+    describe(str(assert_parity(host(out), eo, ro, FWD_TOL["fp16"], "out", "fp16", plain=True)))
+    # and nearer to the reference's fp32-summary result than to its fp16-summary one
+    r16, _, _ = O.forward(q, k, v, is_causal=causal, part_len=part, dtype="fp16", mode="ref")
+    got = host(out)
+    assert np.mean(got == np.asarray(ro, np.float64)) > np.mean(got == np.asarray(r16, np.float64))
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_two_pass_structure(causal):
     """Phase 1 writes P>1 summaries per row to HBM; Phase 2 alone turns them into the output

@@ -11,7 +11,8 @@ move the result by far more than that, so a ``ref`` mode without it would fail.
 Rounding points (src/elsa_twopass_clean/ in the reference):
   * q scaled in fp32 by log2(e)/sqrt(d), then rounded to fp16 (attention_parallel_scan.py:256-259);
   * p = exp2(s - local_max) per 64-key micro-tile, rounded to fp16 for p @ v only; the
-    row sum z adds the fp32 p (:279-283);
+    row sum z adds the fp32 p (:279-283); with summary_dtype=fp32, p @ v takes the fp32 p
+    (SUMMARY_DOT_FP32, :701, :902; attention.py:96-99);
   * the partition summary s stored in fp16 (the s buffer has q's dtype, :476-478);
   * backward: ds = p (dp - D) cast to the input dtype before dq/dk (attention_bwd.py:404, :514),
     p cast to the input dtype before dv (:512).
@@ -32,15 +33,21 @@ def _f16(x):
     return np.asarray(x, np.float64).astype(np.float16).astype(np.float64)
 
 
-def _hand_partition(q, k, v, k0, k1, *, round_q=True, round_p=True, micro=64):
-    """One head: (m, z, s) of keys [k0, k1) for every query row, row by row in float64."""
+def _hand_partition(q, k, v, k0, k1, *, round_q=True, round_p=True, micro=64, generic=False):
+    """One head: (m, z, s) of keys [k0, k1) for every query row, row by row in float64.
+
+    generic: the summary kernel's scoring (attention.py:72, :89): (q . k) * scale, then
+    times log2(e), with q unscaled and unrounded (round_q is ignored)."""
     n_rows, d = q.shape
     ls = np.float32(LOG2E / math.sqrt(d))
     out_m, out_z, out_s = np.empty(n_rows), np.empty(n_rows), np.empty((n_rows, d))
     for i in range(n_rows):
-        qi = (q[i].astype(np.float32) * ls).astype(np.float64)
-        if round_q:
-            qi = _f16(qi)
+        if generic:
+            qi = q[i].astype(np.float64) * (LOG2E / math.sqrt(d))
+        else:
+            qi = (q[i].astype(np.float32) * ls).astype(np.float64)
+            if round_q:
+                qi = _f16(qi)
         m_run, z_run, s_run = -np.inf, 0.0, np.zeros(d)
         for t0 in range(k0, k1, micro):
             t1 = min(t0 + micro, k1)
@@ -97,6 +104,50 @@ def test_phase1_summary_matches_hand_fold(case, k0, k1):
     for kw in ({"round_p": False}, {"round_q": False}):
         _, _, s_mut = _hand_partition(q, k, v, k0, k1, **kw)
         assert _rms_rel(s_mut, hs) >= DROPPED, kw
+
+
+@pytest.mark.parametrize("k0,k1", [(0, 128), (128, 192)])
+def test_fp32_summaries_keep_p_unrounded(case, k0, k1):
+    """fp16 inputs with summary_dtype=fp32: the reference launches its generic summary kernel
+    with SUMMARY_DOT_FP32 (attention_parallel_scan.py:701, :902), which forms p @ v from the
+    fp32 p (attention.py:96-99), and scales fp32 scores after the dot (attention.py:72)."""
+    q, k, v = case
+    rows = np.arange(q.shape[0])
+    m, z, s = O.phase1_partition(q[None].astype(np.float32), k[None].astype(np.float32), v[None].astype(np.float32),
+                                 row_idx=rows, k_begin=k0, k_end=k1, n_ctx=q.shape[0], is_causal=False, bias=None,
+                                 dtype="fp16", mode="ref", generic=True, summary_dtype="fp32")
+    hm, hz, hs = _hand_partition(q, k, v, k0, k1, round_p=False, generic=True)
+    assert np.abs(m[0] - hm).max() <= 1e-5
+    assert _rms_rel(z[0], hz) <= FAITHFUL
+    faithful = _rms_rel(s[0], hs)
+    assert faithful <= FAITHFUL, faithful
+    # the same fold with p rounded to fp16 (the 16-bit-summary rule) is far outside that
+    _, _, s_mut = _hand_partition(q, k, v, k0, k1, round_p=True, generic=True)
+    assert _rms_rel(s_mut, hs) >= DROPPED
+    # and so is the oracle's own 16-bit-summary fold of the same partition
+    _, _, s16 = O.phase1_partition(q[None].astype(np.float32), k[None].astype(np.float32),
+                                   v[None].astype(np.float32), row_idx=rows, k_begin=k0, k_end=k1,
+                                   n_ctx=q.shape[0], is_causal=False, bias=None, dtype="fp16", mode="ref",
+                                   generic=True, summary_dtype="fp16")
+    assert _rms_rel(s16[0], hs) >= DROPPED
+
+
+def test_forward_with_fp32_summaries_stores_them_unrounded(case):
+    """forward(summary_dtype="fp32") on fp16 inputs: summaries merged in fp32, out in fp16."""
+    q, k, v = case
+    n = q.shape[0]
+    out, _, rz = O.forward(q[None, None], k[None, None], v[None, None], part_len=128, dtype="fp16", mode="ref",
+                           summary_dtype="fp32")
+    (m0, z0, s0), (m1, z1, s1) = (_hand_partition(q, k, v, a, min(n, a + 128), round_p=False, generic=True)
+                                  for a in (0, 128))
+    mx = np.maximum(m0, m1)
+    a, b = np.exp2(m0 - mx), np.exp2(m1 - mx)
+    z = z0 * a + z1 * b
+    hand = (s0 * a[:, None] + s1 * b[:, None]) / z[:, None]
+    o = out[0, 0].astype(np.float64)
+    assert np.array_equal(o, _f16(o))
+    assert np.mean(o == _f16(hand)) >= 0.98
+    np.testing.assert_allclose(rz[0], z, rtol=1e-5)
 
 
 def test_forward_rounds_summaries_and_output(case):

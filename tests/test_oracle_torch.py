@@ -146,3 +146,19 @@ def test_key_columns_are_the_full_backward_restricted(causal, bias):
                                     row_chunk=33)
     np.testing.assert_allclose(_np(kk), _np(dk)[:, :, keys], rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(_np(vv), _np(dv)[:, :, keys], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_fp32_summaries_agree_with_numpy_oracle(causal):
+    """fp16 inputs with summary_dtype=fp32 (p @ v from the fp32 p in both restatements)."""
+    q, k, v = O.make_inputs((1, 2, 197, 64), seed=91, dtype="fp16")
+    o1, m1, z1 = O.forward(q, k, v, is_causal=causal, part_len=64, dtype="fp16", mode="ref", summary_dtype="fp32")
+    o2, m2, z2 = T.forward(q, k, v, is_causal=causal, part_len=64, dtype="fp16", mode="ref", summary_dtype="fp32")
+    o1, o2 = np.asarray(o1, np.float64), _np(o2).astype(np.float64)
+    assert np.mean(o1 == o2) >= 0.99
+    assert np.abs(o1 - o2).max() <= 2.0 ** -10 * np.abs(o1).max()
+    np.testing.assert_allclose(*_same_inf(_np(m2), m1), atol=1e-5)
+    np.testing.assert_allclose(_np(z2), z1, rtol=1e-5)
+    # and both differ from the 16-bit-summary fold, whose p @ v rounds p
+    o3, _, _ = T.forward(q, k, v, is_causal=causal, part_len=64, dtype="fp16", mode="ref", summary_dtype="fp16")
+    assert np.mean(_np(o3).astype(np.float64) == o2) < 0.9
