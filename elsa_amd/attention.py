@@ -87,10 +87,9 @@ def _canonical_bias(
     return _BiasMeta(view, int(stride_b), int(stride_h), int(view.stride(2)), int(view.stride(3)), True)
 
 
-def _paper_scan_defaults(
+def _user_tiles(
     *,
     dtype: torch.dtype,
-    seq_len: int,
     head_dim: int,
     block_m: Optional[int],
     block_n: Optional[int],
@@ -99,46 +98,24 @@ def _paper_scan_defaults(
     phase2_warps: Optional[int],
     phase1_stages: Optional[int],
     phase2_stages: Optional[int],
-) -> tuple[int, int, int, int, int, int, int]:
-    """The reference routing table (attention.py:162-236), kept for its validation and clamping.
+) -> tuple[Optional[int], Optional[int]]:
+    """What the reference's routing (attention.py:162-236, :302) does to user-given knobs.
 
-    Only user-supplied ``block_n`` / ``q_chunk_size`` reach the HIP planner; the
-    defaults returned here are the reference's Triton tiles and are not used to
-    launch anything.
+    Warps must be 1, 2, 4 or 8 and stages convert to int (the reference's validation);
+    ``block_n`` and ``q_chunk_size`` are clamped to at least 16, and ``q_chunk_size`` is
+    rounded down to a multiple of block_m (the reference's default: 32 rows for fp32 or head
+    dims above 64, else 64), but not below it.  Returns (partition_len, q_chunk), None
+    where the caller gave nothing: the HIP planner routes those itself.
     """
-    if dtype == torch.float32:
-        if head_dim <= 64:
-            default_block_m = 32
-            if seq_len <= 512:
-                default_block_n = 256
-            elif seq_len < 2048:
-                default_block_n = ((seq_len + 63) // 64) * 64
-            else:
-                default_block_n = 2048
-        else:
-            default_block_m = 32
-            default_block_n = 64
-        default_q_chunk = 512 if seq_len >= 4096 else 1024
-        default_phase1_stages = 2
-    elif dtype == torch.float16 and head_dim == 64 and seq_len >= 8192:
-        default_block_m = 64
-        default_block_n = 2048
-        default_q_chunk = 4096 if seq_len >= 16384 else 2048
-        default_phase1_stages = 1
-    else:
-        default_block_m = 64 if head_dim <= 64 else 32
-        default_block_n = 256 if head_dim <= 64 else 64
-        default_q_chunk = 1024 if seq_len >= 4096 else min(seq_len, 1024)
-        default_phase1_stages = 2
-    return (
-        max(16, int(default_block_m if block_m is None else block_m)),
-        max(16, int(default_block_n if block_n is None else block_n)),
-        max(16, int(default_q_chunk if q_chunk_size is None else q_chunk_size)),
-        _validate_warps("phase1_warps", 4 if phase1_warps is None else phase1_warps),
-        _validate_warps("phase2_warps", 4 if phase2_warps is None else phase2_warps),
-        max(1, int(default_phase1_stages if phase1_stages is None else phase1_stages)),
-        max(1, int(1 if phase2_stages is None else phase2_stages)),
-    )
+    _validate_warps("phase1_warps", 4 if phase1_warps is None else phase1_warps)
+    _validate_warps("phase2_warps", 4 if phase2_warps is None else phase2_warps)
+    for stages in (phase1_stages, phase2_stages):
+        if stages is not None:
+            int(stages)
+    bm = max(16, int(block_m)) if block_m is not None else (32 if dtype == torch.float32 or head_dim > 64 else 64)
+    bn = None if block_n is None else max(16, int(block_n))
+    qc = None if q_chunk_size is None else max(bm, (max(16, int(q_chunk_size)) // bm) * bm)
+    return bn, qc
 
 
 def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, who: str) -> None:
@@ -271,14 +248,10 @@ def _resolve_forward_options(q, *, block_m, block_n, q_chunk_size, summary_dtype
         summary_dtype = torch.float32 if q.dtype == torch.float32 else q.dtype
     if summary_dtype not in (torch.float16, torch.bfloat16, torch.float32):
         raise ValueError("summary_dtype must be fp16, bf16, or fp32")
-    _, seq_len, _, head_dim = (None, int(q.shape[2]), None, int(q.shape[3]))
-    bm, bn, qc, *_ = _paper_scan_defaults(
-        dtype=q.dtype, seq_len=seq_len, head_dim=head_dim, block_m=block_m, block_n=block_n,
-        q_chunk_size=q_chunk_size, phase1_warps=phase1_warps, phase2_warps=phase2_warps,
-        phase1_stages=phase1_stages, phase2_stages=phase2_stages,
-    )
-    qc = max(bm, (qc // bm) * bm)  # attention.py:302
-    return (bn if block_n is not None else None), (qc if q_chunk_size is not None else None), summary_dtype
+    bn, qc = _user_tiles(dtype=q.dtype, head_dim=int(q.shape[3]), block_m=block_m, block_n=block_n,
+                         q_chunk_size=q_chunk_size, phase1_warps=phase1_warps, phase2_warps=phase2_warps,
+                         phase1_stages=phase1_stages, phase2_stages=phase2_stages)
+    return bn, qc, summary_dtype
 
 
 def twopass_attention(

@@ -274,17 +274,23 @@ def test_python_api_validation_on_cpu_tensors():
         elsa_amd.twopass_attention_backward(q, q, q, q, q[:, :1])
 
 
-def test_reference_defaults_and_warps_validation():
-    from elsa_amd.attention import _paper_scan_defaults, _validate_warps
+def test_user_tiles_and_warps_validation():
+    from elsa_amd.attention import _user_tiles, _validate_warps
 
-    assert _paper_scan_defaults(dtype=torch.float16, seq_len=16384, head_dim=64, block_m=None, block_n=None,
-                                q_chunk_size=None, phase1_warps=None, phase2_warps=None, phase1_stages=None,
-                                phase2_stages=None) == (64, 2048, 4096, 4, 4, 1, 1)
-    assert _paper_scan_defaults(dtype=torch.float32, seq_len=1000, head_dim=64, block_m=None, block_n=None,
-                                q_chunk_size=None, phase1_warps=None, phase2_warps=None, phase1_stages=None,
-                                phase2_stages=None)[:3] == (32, 1024, 1024)
+    kw = dict(block_m=None, block_n=None, q_chunk_size=None, phase1_warps=None, phase2_warps=None,
+              phase1_stages=None, phase2_stages=None)
+    # nothing given: the HIP planner routes
+    assert _user_tiles(dtype=torch.float16, head_dim=64, **kw) == (None, None)
+    # attention.py:302: q_chunk rounded down to the default block_m (64 for fp16 d <= 64, 32 for
+    # fp32 or d > 64), never below it; block_n and q_chunk clamped to >= 16 (:228-236)
+    assert _user_tiles(dtype=torch.float16, head_dim=64, **dict(kw, block_n=8, q_chunk_size=3000)) == (16, 2944)
+    assert _user_tiles(dtype=torch.float32, head_dim=64, **dict(kw, q_chunk_size=3000)) == (None, 2976)
+    assert _user_tiles(dtype=torch.float16, head_dim=128, **dict(kw, q_chunk_size=40)) == (None, 32)
+    assert _user_tiles(dtype=torch.float16, head_dim=64, **dict(kw, block_m=128, q_chunk_size=300)) == (None, 256)
     with pytest.raises(ValueError, match="1, 2, 4, or 8"):
         _validate_warps("phase1_warps", 3)
+    with pytest.raises(ValueError, match="1, 2, 4, or 8"):
+        _user_tiles(dtype=torch.float16, head_dim=64, **dict(kw, phase2_warps=16))
 
 
 def test_canonical_bias_cpu():
