@@ -2,6 +2,9 @@
 device sees identical values; the oracle is the checker)."""
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 import torch
 
@@ -41,7 +44,24 @@ def ulp(x, dtype: str) -> np.ndarray:
     return np.spacing(a.astype(np.float32)).astype(np.float64)
 
 
-def assert_parity(got, exact, ref, tol: float, what: str = "", dtype: str = "fp16") -> dict:
+def parity_record(rec: dict) -> None:
+    """Append one parity record (a JSON line) to $ELSA_PARITY_LOG when that is set."""
+    path = os.environ.get("ELSA_PARITY_LOG")
+    if not path:
+        return
+    rec = dict(rec, test=os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0])
+    with open(path, "a") as f:
+        f.write(json.dumps(rec) + "\n")
+
+
+# Factor on the reference's own error in the bar against the exact value: a different but
+# equally accurate evaluation lands within about that multiple of it.  16-bit outputs keep
+# 1.25; fp32 gradients of order 1 and fp32 dbias sums (two float32 summation orders, each a
+# few ulps of 1e-6 scale) take 2.
+EXACT_FACTOR = {"fp16": 1.25, "bf16": 1.25, "fp32": 2.0}
+
+
+def assert_parity(got, exact, ref, tol: float, what: str = "", dtype: str = "fp16", plain: bool = False) -> dict:
     """The parity bar of this build.
 
     ``ref`` is the oracle at the reference's rounding points (the stand-in for the
@@ -51,22 +71,27 @@ def assert_parity(got, exact, ref, tol: float, what: str = "", dtype: str = "fp1
       1. max(|got - ref| - ulp(ref)) <= max(tol, 2 * e_ref)   (the north-star bar versus the
          reference path; e_ref = max|ref - exact| is the reference's own error, and where
          it exceeds tol/2 two independent roundings can differ by up to twice it);
-      2. max(|got - exact| - ulp(exact)/2) <= max(tol, 2 * e_ref)
+      2. max(|got - exact| - ulp(exact)/2) <= max(tol, EXACT_FACTOR[dtype] * e_ref)
          (in the reference's accuracy class beyond the bar: on short causal rows and
          49-token windows the reference's own fp16 rounding of p / dS / out already exceeds
-         the bar against the exact value, and at fp32 gradients of order 1 the two
-         evaluations' float32 roundings are each a few ulps of 1e-6 scale).
+         the bar against the exact value).
+    ``plain=True`` applies the north-star bar alone (tol, with no e_ref term) to both.
+    The returned dict says under "bound" whether the plain bar held for both criteria
+    ("plain") or the e_ref term was needed ("e_ref").
     """
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     exact = np.asarray(exact, np.float64)
     assert got.shape == ref.shape == exact.shape
     e_ref = max_abs(ref, exact)
-    d_ref = float((np.abs(got - ref) - ulp(ref, dtype)).max())
-    e_got = float((np.abs(got - exact) - 0.5 * ulp(exact, dtype)).max())
+    d_ref = float((np.abs(got - ref) - ulp(ref, dtype)).max()) if got.size else 0.0
+    e_got = float((np.abs(got - exact) - 0.5 * ulp(exact, dtype)).max()) if got.size else 0.0
+    bar_ref = tol if plain else max(tol, 2.0 * e_ref)
+    bar_exact = tol if plain else max(tol, EXACT_FACTOR[dtype] * e_ref)
     info = {"vs_ref_beyond_ulp": d_ref, "vs_exact_beyond_half_ulp": e_got, "ref_vs_exact": e_ref,
-            "vs_ref_raw": max_abs(got, ref)}
-    assert d_ref <= max(tol, 2.0 * e_ref), (what, info)
-    assert e_got <= max(tol, 2.0 * e_ref), (what, info)
+            "vs_ref_raw": max_abs(got, ref), "tol": tol,
+            "bound": "plain" if (d_ref <= tol and e_got <= tol) else "e_ref"}
+    parity_record(dict(info, what=what, dtype=dtype, plain=plain, n=int(got.size)))
+    assert d_ref <= bar_ref, (what, info)
+    assert e_got <= bar_exact, (what, info)
     return info
-

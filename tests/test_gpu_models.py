@@ -10,10 +10,18 @@ import pytest
 import torch
 
 import elsa_amd
-from elsa_amd.vision_models import swin_tiny_patch4_window7, vit_tiny_patch16
+from elsa_amd.vision_models import SwinTransformer, swin_tiny_patch4_window7, vit_tiny_patch16
 from tests.gpu_util import describe
 
 pytestmark = pytest.mark.gpu
+
+
+def swin_tiny_window_ratio8(img_size: int) -> SwinTransformer:
+    """Swin-T at the reference benchmark's geometry: window = (img/4) / window_ratio with
+    window_ratio 8 (benchmarks/bench_timm_dropin.py:38-49, :60), so 12x12 windows (144 tokens)
+    at 384 px and 16x16 (256 tokens) at 512 px, shifted, with the relative-position bias."""
+    return SwinTransformer(img_size=img_size, embed_dim=96, depths=(2, 2, 6, 2), num_heads=(3, 6, 12, 24),
+                           window_size=img_size // 4 // 8)
 
 
 def _models(builder, img, dtype, train=False):
@@ -28,8 +36,11 @@ def _models(builder, img, dtype, train=False):
 @pytest.mark.parametrize("dt,tol", [(torch.float32, 2e-4), (torch.float16, 2e-2)])
 @pytest.mark.parametrize("builder,img,batch", [(vit_tiny_patch16, 224, 2), (swin_tiny_patch4_window7, 224, 2),
                                                (vit_tiny_patch16, 512, 2), (vit_tiny_patch16, 1024, 8),
+                                               (vit_tiny_patch16, 2048, 2),  # 16385 tokens: B2 H3 N16385
                                                (swin_tiny_patch4_window7, 384, 8),
-                                               (swin_tiny_patch4_window7, 512, 8)])
+                                               (swin_tiny_patch4_window7, 512, 8),
+                                               (swin_tiny_window_ratio8, 384, 4),
+                                               (swin_tiny_window_ratio8, 512, 4)])
 def test_dropin_forward_matches_sdpa(builder, img, batch, dt, tol):
     describe(f"dropin fwd {builder.__name__} {img} batch {batch} {dt}")
     ref, elsa = _models(builder, img, dt)
@@ -42,15 +53,24 @@ def test_dropin_forward_matches_sdpa(builder, img, batch, dt, tol):
     assert err <= tol * max(1.0, want.abs().max().item())
 
 
-@pytest.mark.parametrize("builder,img", [(vit_tiny_patch16, 224), (swin_tiny_patch4_window7, 224)])
-def test_dropin_training_gradients_match_sdpa(builder, img):
-    describe(f"dropin train {builder.__name__} {img}")
+# the training step above 224 px at the reference's published training sizes (README.md:73-76:
+# ViT 384/512/768, Swin 384/512) and BASELINE's ViT 1024 / 2048 px rows
+TRAIN_FP32 = [(vit_tiny_patch16, 224, 2), (swin_tiny_patch4_window7, 224, 2), (vit_tiny_patch16, 512, 2),
+              (vit_tiny_patch16, 1024, 2), (vit_tiny_patch16, 2048, 1), (swin_tiny_patch4_window7, 384, 2),
+              (swin_tiny_patch4_window7, 512, 2), (swin_tiny_window_ratio8, 384, 2),
+              (swin_tiny_window_ratio8, 512, 2)]
+
+
+@pytest.mark.parametrize("builder,img,batch", TRAIN_FP32,
+                         ids=[f"{b.__name__}-{i}-b{n}" for b, i, n in TRAIN_FP32])
+def test_dropin_training_gradients_match_sdpa(builder, img, batch):
+    describe(f"dropin train {builder.__name__} {img} batch {batch}")
     ref, elsa = _models(builder, img, torch.float32, train=True)
     ref.train()
     elsa.train()
     g = torch.Generator().manual_seed(11)
-    x = torch.randn(2, 3, img, img, generator=g).cuda()
-    labels = torch.randint(0, 1000, (2,), generator=g).cuda()
+    x = torch.randn(batch, 3, img, img, generator=g).cuda()
+    labels = torch.randint(0, 1000, (batch,), generator=g).cuda()
     for m in (ref, elsa):
         torch.nn.functional.cross_entropy(m(x), labels).backward()
     worst = 0.0
@@ -62,22 +82,28 @@ def test_dropin_training_gradients_match_sdpa(builder, img):
     describe(f"  worst relative grad error {worst:.3e}")
 
 
-@pytest.mark.parametrize("builder", [vit_tiny_patch16, swin_tiny_patch4_window7])
-def test_dropin_fp16_training_is_as_accurate_as_sdpa_fp16(builder):
-    """fp16 training step at 224 px, batch 8: the gradients of the fp16 model with the ELSA
-    drop-in and of the same fp16 model on SDPA, each against the fp32 SDPA model; ELSA's
-    error may not exceed twice SDPA's (fp16 rounding everywhere else in the network sets both)."""
-    describe(f"dropin fp16 train {builder.__name__} 224")
+TRAIN_FP16 = [(vit_tiny_patch16, 224, 8), (swin_tiny_patch4_window7, 224, 8), (vit_tiny_patch16, 512, 8),
+              (vit_tiny_patch16, 1024, 4), (vit_tiny_patch16, 2048, 1), (swin_tiny_patch4_window7, 384, 8),
+              (swin_tiny_patch4_window7, 512, 8), (swin_tiny_window_ratio8, 512, 4)]
+
+
+@pytest.mark.parametrize("builder,img,batch", TRAIN_FP16,
+                         ids=[f"{b.__name__}-{i}-b{n}" for b, i, n in TRAIN_FP16])
+def test_dropin_fp16_training_is_as_accurate_as_sdpa_fp16(builder, img, batch):
+    """fp16 training step: the gradients of the fp16 model with the ELSA drop-in and of the
+    same fp16 model on SDPA, each against the fp32 SDPA model; ELSA's error may not exceed
+    twice SDPA's (fp16 rounding everywhere else in the network sets both)."""
+    describe(f"dropin fp16 train {builder.__name__} {img} batch {batch}")
     torch.manual_seed(1234)
-    base = builder(224)
+    base = builder(img)
     elsa = copy.deepcopy(base)
     elsa_amd.patch_timm_attention_train(elsa)
     ref32 = copy.deepcopy(base).cuda().train()
     sdpa16 = copy.deepcopy(base).to("cuda", torch.float16).train()
     elsa16 = elsa.to("cuda", torch.float16).train()
     g = torch.Generator().manual_seed(12)
-    x = torch.randn(8, 3, 224, 224, generator=g).cuda()
-    labels = torch.randint(0, 1000, (8,), generator=g).cuda()
+    x = torch.randn(batch, 3, img, img, generator=g).cuda()
+    labels = torch.randint(0, 1000, (batch,), generator=g).cuda()
     for m, xx in ((ref32, x), (sdpa16, x.half()), (elsa16, x.half())):
         torch.nn.functional.cross_entropy(m(xx).float(), labels).backward()
     errs = {"sdpa16": 0.0, "elsa16": 0.0}
