@@ -333,7 +333,9 @@ void bwd_dkdv_kernel(const BwdParams p) {
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
-  const WgCoord wg = xcd_order();
+  // causal: the work of a key block shrinks with its index (heaviest first; paired heavy with
+  // light where the grid fits in one round)
+  const WgCoord wg = (p.causal && WAVES == 4) ? xcd_order_paired() : xcd_order();
   const int bh = wg.y;
   const int wg_key0 = wg.x * BN;
   const int key0 = wg_key0 + wave * 32;
@@ -526,8 +528,8 @@ void bwd_dq_half_kernel(const BwdParams p) {
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
   // causal: the work of a row block grows with its index; each XCD takes its range of
-  // row blocks heaviest first
-  WgCoord wg = xcd_order();
+  // row blocks heaviest first (paired heavy with light where the grid fits in one round)
+  WgCoord wg = (p.causal && WAVES == 4) ? xcd_order_paired() : xcd_order();
   if (p.causal) wg.x = (int)gridDim.x - 1 - wg.x;
   const int bh = wg.y;
   const int wg_row0 = wg.x * BM;
@@ -576,6 +578,28 @@ void bwd_dq_half_kernel(const BwdParams p) {
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) ndd[rt][r] = SEED_D ? -dd[rt] : 0.f;
+  // The two-tile kernel (no registers for the seeds) adds -D with one more MFMA per row tile and
+  // sub-tile instead: A = 1 at k = 0, 1 for every key, B = (-D_hi, -D_lo) of the lane's row at
+  // k = 0, 1, where D_hi = D rounded to T and D_lo = D - D_hi rounded to T (D to ~22 bits for fp16,
+  // ~16 for bf16).  The vector work per score loses its subtract; the matrix work gains 1 MFMA in 12
+  // (the 8-wave kernel then spills 12 bytes per lane).  B1 H8 16K d64: dq 0.740 -> 0.720 ms (fp16),
+  // 0.702 -> 0.684 ms (bf16); B2 H8 8K 0.384 -> 0.372 ms.
+  constexpr bool MFMA_D = !HAS_BIAS && DP <= 64 && RT == 2;
+  F ones_a{}, nd_b[MFMA_D ? RT : 1];
+  if constexpr (MFMA_D) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) nd_b[rt] = F{};
+    if (g == 0) {
+      ones_a[0] = static_cast<T>(1.f);
+      ones_a[1] = static_cast<T>(1.f);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const T hi = static_cast<T>(-dd[rt]);
+        nd_b[rt][0] = hi;
+        nd_b[rt][1] = static_cast<T>(-dd[rt] - static_cast<float>(hi));
+      }
+    }
+  }
 
   // element offsets of this thread's staging chunks inside a stage (row strides are
   // below 2^25 elements, checked by the API, so 64 rows fit in 32 bits)
@@ -644,6 +668,7 @@ static_for<0, NCH>([&](auto I) {
             s = M::mma(kf[kk], qf[rt][kk], s);
             dp = M::mma(vf[kk], gf[rt][kk], dp);
           }
+          if constexpr (MFMA_D) dp = M::mma(ones_a, nd_b[rt], dp);
           const int my_row = row0 + rt * 32 + c;
           const bool full = (t0 + KT <= k_end) && (!p.causal || t0 + KT - 1 <= row0 + rt * 32);
           const float nl = -lse[rt];
@@ -668,7 +693,7 @@ static_for<0, NCH>([&](auto I) {
               }
             }
 #pragma unroll
-            for (int r = 0; r < 16; ++r) ds[r] *= SEED_D ? dp[r] : dp[r] - dd[rt];
+            for (int r = 0; r < 16; ++r) ds[r] *= (SEED_D || MFMA_D) ? dp[r] : dp[r] - dd[rt];
           }
 #pragma unroll
           for (int j = 0; j < 2; ++j)
@@ -781,7 +806,9 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
-  const WgCoord wg = xcd_order();
+  // causal: the work of a key block shrinks with its index (heaviest first; paired heavy with
+  // light where the grid fits in one round)
+  const WgCoord wg = (p.causal && WAVES == 4) ? xcd_order_paired() : xcd_order();
   const int bh = wg.y;
   const int wg_key0 = wg.x * BN;
   const int key0 = wg_key0 + wave * KEYS_W;

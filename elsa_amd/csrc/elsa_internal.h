@@ -112,8 +112,11 @@ struct BwdParams {
 
 // Ranges the fp16/bf16 backward cuts its loops into when its unsplit grid (128 rows or keys per
 // work-group) leaves the chip under-filled: 1 (no split) unless fewer than 512 work-groups, then
-// doubled while that stays short of 512 and every range keeps at least 256 rows.  fp32, biased
-// calls and head dims above 64 keep 1.
+// doubled while that stays short of 512 and n / (2 * split) is at least 256.  Each range is
+// split_len = ceil(n / split) rounded up to whole 64-row stages, so the last one can be shorter
+// (B8 H3 N1025: 320, 320, 320 and 65 rows); the launch lasts as long as the longest range,
+// which no choice of whole-stage ranges makes shorter.  fp32, biased calls and head dims above
+// 64 keep 1.
 int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias);
 
 // stage < 0: preprocess, dq and dk/dv; 0: preprocess only; 1: dq only; 2: dk/dv only.

@@ -192,6 +192,21 @@ __device__ inline WgCoord xcd_order() {
   const int gx = gridDim.x, gy = gridDim.y, l = xcd_linear();
   return {l % gx, (l / gx) % gy, l / (gx * gy)};
 }
+// xcd_order for causal backward grids that fit the chip in one round of two work-groups per CU
+// (more than 256, at most 512 work-groups of the 4-wave kernels), whose work-groups are numbered
+// heaviest first within each head: the second half of each XCD's work-groups comes lightest
+// first, so that the CU that takes the j-th work-group of the first half also takes the j-th
+// lightest, and every CU gets about the same work.
+__device__ inline WgCoord xcd_order_paired() {
+  const int n = gridDim.x * gridDim.y * gridDim.z;
+  const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const int per = n >> 3, rem = n & 7, xcd = lin & 7;
+  int slot = lin >> 3;
+  if (n > 256 && n <= 512 && rem == 0 && (per & 1) == 0 && slot >= per / 2) slot = per + per / 2 - 1 - slot;
+  const int l = xcd * per + min(xcd, rem) + slot;
+  const int gx = gridDim.x, gy = gridDim.y;
+  return {l % gx, (l / gx) % gy, l / (gx * gy)};
+}
 // Non-causal Phase 1 (grid x = row block, y = head, z = K partition) with the panels (head,
 // partition) dealt to the XCDs in turn, each panel whole: the dispatcher sends workgroup L to
 // XCD L % 8, and the j-th workgroup of an XCD (j = L / 8) takes row block j % gx of panel
