@@ -62,9 +62,8 @@ def _args():
                     help="ViT-Tiny image sizes for the img/s fields in --dtype (empty: skip)")
     ap.add_argument("--swin-img", type=int, nargs="*", default=[224, 384, 512],
                     help="Swin-Tiny image sizes for the img/s fields in --dtype (empty: skip)")
-    # the same models in fp32 as second fields (ViT up to 1024 px, the sizes of the reference's
-    # fp32 ViT table, README.md:65, 74)
-    ap.add_argument("--vit-img-fp32", type=int, nargs="*", default=[224, 512, 1024],
+    # the same models in fp32 as second fields (BASELINE config 4's four ViT sizes in fp32 too)
+    ap.add_argument("--vit-img-fp32", type=int, nargs="*", default=[224, 512, 1024, 2048],
                     help="ViT-Tiny image sizes of the fp32 fields (empty: skip)")
     ap.add_argument("--swin-img-fp32", type=int, nargs="*", default=[224, 384, 512],
                     help="Swin-Tiny image sizes of the fp32 fields (empty: skip)")
@@ -417,23 +416,28 @@ def main() -> int:
             kernels[name] = {"ms": round(ms, 4), "gbps": round(ach, 1), "frac_peak": round(ach / HBM_GBPS, 4)}
     dom = max(kern_ms, key=kern_ms.get)
     bound, work = algo[dom]
+    # HBM bytes per launch come from rocprofv3 counters, which this run does not collect: the
+    # figure of the committed profile (FETCH_SIZE + WRITE_SIZE of this kernel, calibrated), valid
+    # while the kernels are the ones profiled there
     traffic = None
+    traffic_source = None
     if os.path.exists(args.traffic_file):
         try:
             with open(args.traffic_file) as fh:
                 traffic = json.load(fh).get(dom, {}).get("hbm_bytes_per_launch")
+            traffic_source = os.path.relpath(args.traffic_file, ROOT) + " (committed rocprofv3 --pmc profile)"
         except (OSError, ValueError):
             traffic = None
     if bound == "mfma":
         achieved = work / (kern_ms[dom] * 1e-3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
-                    "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": dom,
-                    "work_per_launch": work}
+                    "frac": round(achieved / peak, 4), "traffic": traffic, "traffic_source": traffic_source,
+                    "kernel": dom, "work_per_launch": work}
     else:
         achieved = work / (kern_ms[dom] * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_GBPS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_GBPS, 4), "traffic": traffic, "kernel": dom,
-                    "work_per_launch": work}
+                    "frac": round(achieved / HBM_GBPS, 4), "traffic": traffic, "traffic_source": traffic_source,
+                    "kernel": dom, "work_per_launch": work}
 
     value = (f_fwd + f_bwd) / (ms_step * 1e-3) / 1e12
     result = {
@@ -576,19 +580,39 @@ def _vision_bench(args, dt, builder, imgs, label, tokens):
         x = torch.randn(args.vit_batch, 3, img, img, device="cuda", dtype=dt)
         labels = torch.randint(0, 1000, (args.vit_batch,), device="cuda")
         row = {"tokens": tokens(img)}
+        # fp32 beyond 4K tokens: fewer timed iterations (a ViT-T fp32 training step at 16385 tokens
+        # takes most of a second)
+        steps = args.vit_steps
+        if dt == torch.float32 and tokens(img) > 4097:
+            steps = max(2, args.vit_steps * 4097 // tokens(img))
+        row["steps"] = steps
         for name, m in models.items():
             m.eval()
-            row[f"{name}_fwd_ms"] = _graph_fwd_ms(m, x, args.vit_steps)
+            row[f"{name}_fwd_ms"] = _unless_oom(lambda: _graph_fwd_ms(m, x, steps))
         for name, m in (("sdpa", models["sdpa"]), ("elsa", elsa_train.to("cuda", dt))):
-            row[f"{name}_train_ms"] = _train_ms(m, x, labels, args.vit_steps)
+            row[f"{name}_train_ms"] = _unless_oom(lambda: _train_ms(m, x, labels, steps))
         for kind in ("fwd", "train"):
-            row[f"elsa_{kind}_img_s"] = round(args.vit_batch / (row[f"elsa_{kind}_ms"] * 1e-3), 1)
-            row[f"{kind}_lat_ratio_vs_sdpa"] = round(row[f"elsa_{kind}_ms"] / row[f"sdpa_{kind}_ms"], 3)
+            e, b = row[f"elsa_{kind}_ms"], row[f"sdpa_{kind}_ms"]
+            row[f"elsa_{kind}_img_s"] = round(args.vit_batch / (e * 1e-3), 1) if e else None
+            row[f"{kind}_lat_ratio_vs_sdpa"] = round(e / b, 3) if e and b else None
         print(f"bench: {builder.__name__} {img}px {row}", file=sys.stderr, flush=True)
         out[str(img)] = row
         del models, elsa_train
         torch.cuda.empty_cache()
     return out
+
+
+def _unless_oom(fn):
+    """fn() in ms, or None where it ran out of device memory (PyTorch's SDPA math path keeps
+    every layer's [B, H, N, N] attention matrix for the backward)."""
+    import torch
+
+    try:
+        return fn()
+    except torch.cuda.OutOfMemoryError:
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        return None
 
 
 def _graph_fwd_ms(model, x, steps):

@@ -1308,7 +1308,7 @@ int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias) {
 }
 
 // out[b, h, n, d] = scale * sum over the split ranges of part[z][b*H + h][n][d], 4 head-dim
-// elements per thread (head dims are multiples of 8); grid y picks one of up to two such sums
+// elements per thread (head dims are multiples of 8); grid y picks one of up to three such sums
 struct CombineOut {
   const float* part;
   void* out;
@@ -1316,9 +1316,9 @@ struct CombineOut {
   float scale;
 };
 template <typename T>
-__global__ __launch_bounds__(256) void bwd_combine_kernel(CombineOut c0, CombineOut c1, int split, int64_t sstride,
-                                                          int H, int N, int D, int dp) {
-  const CombineOut& cj = blockIdx.y ? c1 : c0;
+__global__ __launch_bounds__(256) void bwd_combine_kernel(CombineOut c0, CombineOut c1, CombineOut c2, int split,
+                                                          int64_t sstride, int H, int N, int D, int dp) {
+  const CombineOut& cj = blockIdx.y == 0 ? c0 : (blockIdx.y == 1 ? c1 : c2);
   const float* __restrict__ part = cj.part;
   T* __restrict__ out = static_cast<T*>(cj.out);
   const int64_t o0 = cj.os[0], o1 = cj.os[1], o2 = cj.os[2];
@@ -1344,12 +1344,13 @@ __global__ __launch_bounds__(256) void bwd_combine_kernel(CombineOut c0, Combine
   *reinterpret_cast<t4*>(out + (bh / H) * o0 + (bh % H) * o1 + n * o2 + d) = o;
 }
 
+// one launch for up to three sums (n = 1, 2 or 3 of c[0..2])
 template <typename T>
-static hipError_t combine_launch(const BwdParams& p, const CombineOut& c0, const CombineOut* c1, hipStream_t st) {
+static hipError_t combine_launch(const BwdParams& p, const CombineOut* c, int n, hipStream_t st) {
   const int64_t rows = (int64_t)p.BH * p.N;
   const int64_t threads = rows * (p.D / 4);
-  hipLaunchKernelGGL(bwd_combine_kernel<T>, dim3((unsigned)((threads + 255) / 256), c1 ? 2u : 1u), dim3(256), 0, st,
-                     c0, c1 ? *c1 : c0, p.split, rows * p.dp, p.H, p.N, p.D, p.dp);
+  hipLaunchKernelGGL(bwd_combine_kernel<T>, dim3((unsigned)((threads + 255) / 256), (unsigned)n), dim3(256), 0, st,
+                     c[0], c[n > 1 ? 1 : 0], c[n > 2 ? 2 : 0], p.split, rows * p.dp, p.H, p.N, p.D, p.dp);
   return hipGetLastError();
 }
 
@@ -1379,18 +1380,25 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
         // an under-filled grid (short sequences, few heads): the key (dq) or row (dK/dV) loop cut
         // into p.split ranges over grid z, fp32 partials summed by a combine launch
         const dim3 gs(grid.x, grid.y, (unsigned)p.split);
+        const CombineOut cq{p.part, p.dq, {p.dqs[0], p.dqs[1], p.dqs[2]}, p.scale};
+        const CombineOut ck{p.part + p.part_stride, p.dk, {p.dks[0], p.dks[1], p.dks[2]}, p.scale};
+        const CombineOut cv{p.part + 2 * p.part_stride, p.dv, {p.dvs[0], p.dvs[1], p.dvs[2]}, 1.f};
         if (stage < 0 || stage == 1) {
           hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, W, false>), gs, dim3(64 * W), 0, st, p);
           if ((e = hipGetLastError()) != hipSuccess) return e;
-          const CombineOut cq{p.part, p.dq, {p.dqs[0], p.dqs[1], p.dqs[2]}, p.scale};
-          if ((e = combine_launch<T>(p, cq, nullptr, st)) != hipSuccess) return e;
+          if (stage == 1 && (e = combine_launch<T>(p, &cq, 1, st)) != hipSuccess) return e;
         }
         if (stage < 0 || stage == 2) {
           hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, W, false>), gs, dim3(64 * W), 0, st, p);
           if ((e = hipGetLastError()) != hipSuccess) return e;
-          const CombineOut ck{p.part + p.part_stride, p.dk, {p.dks[0], p.dks[1], p.dks[2]}, p.scale};
-          const CombineOut cv{p.part + 2 * p.part_stride, p.dv, {p.dvs[0], p.dvs[1], p.dvs[2]}, 1.f};
-          e = combine_launch<T>(p, ck, &cv, st);
+        }
+        // the whole backward sums the three gradients' partials in one launch
+        if (stage < 0) {
+          const CombineOut all[3] = {cq, ck, cv};
+          e = combine_launch<T>(p, all, 3, st);
+        } else if (stage == 2) {
+          const CombineOut kv[2] = {ck, cv};
+          e = combine_launch<T>(p, kv, 2, st);
         }
         return e;
       }

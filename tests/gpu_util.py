@@ -49,7 +49,8 @@ def parity_record(rec: dict) -> None:
     path = os.environ.get("ELSA_PARITY_LOG")
     if not path:
         return
-    rec = dict(rec, test=os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0])
+    # PYTEST_CURRENT_TEST is "<node id> (<phase>)"; node ids can hold spaces
+    rec = dict(rec, test=os.environ.get("PYTEST_CURRENT_TEST", "").rsplit(" (", 1)[0])
     with open(path, "a") as f:
         f.write(json.dumps(rec) + "\n")
 

@@ -448,3 +448,35 @@ def test_bwd_dbias_matches_bwd_then_dbias(dt, shape, bias_shape, causal):
     # chain of D/2 steps, the dbias kernel's in four; their rounding grows with sqrt(D / 32)
     chain = max(1.0, d / 32) ** 0.5
     assert np.abs(x - y).max() <= 1e-6 * max(1.0, np.abs(y).max()) * pairs ** 0.5 * chain + 1e-7
+
+
+# elsa_bwd_stage 0 / 1 / 2 launched one by one (what bench.py times) against elsa_bwd in one call,
+# which sums the split backward's dq, dK and dV partials in a single combine launch: the same bits.
+@pytest.mark.parametrize("shape,dt,causal", [((1, 8, 1024, 64), "fp16", False), ((8, 3, 1025, 64), "bf16", False),
+                                             ((1, 4, 2048, 64), "fp16", True), ((2, 32, 1024, 64), "fp16", False)])
+def test_backward_stages_one_by_one_are_the_whole_backward(shape, dt, causal):
+    import ctypes
+    import math
+
+    from elsa_amd import _lib
+    from elsa_amd.attention import _BiasMeta
+    from elsa_amd.attention_bwd import _attach_workspace, _bwd_args
+
+    describe(f"backward stages one by one {shape} {dt} causal={causal}")
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(31)
+    q, k, v, do = (torch.randn(shape, generator=g).to(TORCH_DT[dt]).cuda() for _ in range(4))
+    out, rm, rz = elsa_amd.twopass_attention_with_state(q, k, v, is_causal=causal)
+    grads = []
+    for stages in ((-1,), (0, 1, 2)):
+        dq, dk, dv = torch.full_like(q, float("nan")), torch.full_like(k, float("nan")), torch.full_like(v, float("nan"))
+        ba = _bwd_args(q, k, v, out, do, rm, rz, dq, dk, dv, _BiasMeta(None, 0, 0, 0, 0, False), is_causal=causal,
+                       scale=1.0 / math.sqrt(shape[-1]))
+        ws = _attach_workspace(lib, ba, q.device)
+        for st in stages:
+            _lib.check(lib.elsa_bwd_stage(ctypes.byref(ba), st, _lib.stream_handle(q.device)), "elsa_bwd_stage")
+        torch.cuda.synchronize()
+        grads.append((dq, dk, dv))
+        del ws
+    for name, a, b in zip(("dq", "dk", "dv"), *grads):
+        assert not torch.isnan(a).any() and torch.equal(a, b), name
