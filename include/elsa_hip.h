@@ -162,7 +162,9 @@ int elsa_fwd(const elsa_fwd_args* args, void* stream);
  * partitions, q-chunked to fit the array).  A call whose single query row needs more than
  * 64 MiB of summaries (partitions x B*H x (8 + head_dim * summary bytes)) returns
  * ELSA_ERR_WORKSPACE.  `stream` must belong to the current device.  All calls on one GPU share
- * its array: calls that overlap on one GPU race. */
+ * its array: calls that overlap on one GPU race (keep them on one stream).  A device's first call
+ * resolves the array's address (hipGetSymbolAddress): make one eager call on the device before
+ * capturing this entry point into a graph. */
 int elsa_fwd_noalloc(const elsa_fwd_args* args, void* stream);
 /* The two passes separately, for rows [q_start, q_start+q_len) (q_len <= plan.q_chunk). */
 int elsa_phase1(const elsa_fwd_args* args, int32_t q_start, int32_t q_len, void* stream);
