@@ -579,24 +579,31 @@ void bwd_dq_half_kernel(const BwdParams p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) ndd[rt][r] = SEED_D ? -dd[rt] : 0.f;
   // The two-tile kernel (no registers for the seeds) adds -D with one more MFMA per row tile and
-  // sub-tile instead: A = 1 at k = 0, 1 for every key, B = (-D_hi, -D_lo) of the lane's row at
-  // k = 0, 1, where D_hi = D rounded to T and D_lo = D - D_hi rounded to T (D to ~22 bits for fp16,
-  // ~16 for bf16).  The vector work per score loses its subtract; the matrix work gains 1 MFMA in 12
-  // (the 8-wave kernel then spills 12 bytes per lane).  B1 H8 16K d64: dq 0.740 -> 0.720 ms (fp16),
-  // 0.702 -> 0.684 ms (bf16); B2 H8 8K 0.384 -> 0.372 ms.
+  // sub-tile instead: A = (2^15, 1, 1) at k = 0, 1, 2 for every key and B = (b0, b1, b2) of the
+  // lane's row there, with b0 = T(-D / 2^15), r = -D - 2^15 b0, b1 = T(r), b2 = T(r - b1): the
+  // products are exact and their fp32 sum is -D within 2^-22 relative plus 3e-8 absolute (fp16
+  // subnormals), for |D| up to 1.4e8 with fp16 (bf16 has fp32's range); an fp16 -D alone would
+  // overflow past 65504, e.g. under loss-scaled gradients.  The vector work per
+  // score loses its subtract; the matrix work gains 1 MFMA in 12 (the 8-wave kernel then spills 12
+  // bytes per lane).  B1 H8 16K d64: dq 0.740 -> 0.720 ms (fp16), 0.702 -> 0.684 ms (bf16); B2 H8
+  // 8K 0.384 -> 0.372 ms.
   constexpr bool MFMA_D = !HAS_BIAS && DP <= 64 && RT == 2;
   F ones_a{}, nd_b[MFMA_D ? RT : 1];
   if constexpr (MFMA_D) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) nd_b[rt] = F{};
     if (g == 0) {
-      ones_a[0] = static_cast<T>(1.f);
+      ones_a[0] = static_cast<T>(32768.f);
       ones_a[1] = static_cast<T>(1.f);
+      ones_a[2] = static_cast<T>(1.f);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        const T hi = static_cast<T>(-dd[rt]);
-        nd_b[rt][0] = hi;
-        nd_b[rt][1] = static_cast<T>(-dd[rt] - static_cast<float>(hi));
+        const T b0 = static_cast<T>(-dd[rt] * (1.f / 32768.f));
+        const float r = -dd[rt] - static_cast<float>(b0) * 32768.f;
+        const T b1 = static_cast<T>(r);
+        nd_b[rt][0] = b0;
+        nd_b[rt][1] = b1;
+        nd_b[rt][2] = static_cast<T>(r - static_cast<float>(b1));
       }
     }
   }
