@@ -1065,11 +1065,27 @@ void phase1_pp_kernel(const Phase1Params p) {
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const float z_raw = wave_sum_pair(z_lane[rt]);
+    // the relaxed summary, relative to m_run, can be up to 2^kLazyTau times the one relative to the
+    // row maximum: where the row's |s| passes half the fp16 range, an fp16 summary is stored
+    // relative to m_run + kLazyTau instead, no larger than the exact-maximum summary (which the
+    // reference also stores in fp16, attention_parallel_scan.py:476-478)
+    bool shift = false;
+    if constexpr (!EXACT) {
+      if (!p.direct && p.s_dtype == ELSA_F16) {
+        float amax = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) amax = fmaxf(amax, fabsf(oacc[rt][dt][r]));
+        shift = wave_max_pair(amax) > 32768.f;
+      }
+    }
     const int my_row = row0 + rt * 32 + c;
     if (my_row >= q_end) continue;
     // renormalise to the exact row maximum (m_run <= m_true <= m_run + kLazyTau); the
-    // relaxed state keeps the reference m_run, at most kLazyTau below the maximum
-    if constexpr (!EXACT) m_true[rt] = m_run[rt];
+    // relaxed state keeps the reference m_run, at most kLazyTau below the maximum (or
+    // m_run + kLazyTau, at most kLazyTau above it, for a shifted fp16 summary)
+    if constexpr (!EXACT) m_true[rt] = shift ? m_run[rt] + kLazyTau : m_run[rt];
     const float f = (m_true[rt] == kNegInf) ? 1.f : fast_exp2(m_run[rt] - m_true[rt]);
     const int64_t ridx = ((int64_t)kb * p.BH + bh) * p.rows_pad + (my_row - p.q_start);
     const int64_t orow = (int64_t)bh * p.N + my_row;

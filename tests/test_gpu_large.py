@@ -431,3 +431,45 @@ def test_reference_gradient_check_protocol(case):
     for name, gg, e, r in zip(("dq", "dk", "dv"), got[3:], grads_exact, grads_ref):
         info = assert_parity(_np(flat(gg)), _np(e), _np(r), GRAD_TOL[dt], name, dt, plain=True)
         describe(f"  {name} {info}")
+
+
+def test_relaxed_state_fp16_summaries_do_not_overflow():
+    """The relaxed reference can sit up to 8 below a row's maximum, and a partition summary relative
+    to it up to 2^8 times the one relative to the maximum.  Here the first 64 keys score 0 and every
+    later one 2.99 (base 2): the fold keeps the first stage's reference (each lane's 32 exps sum to
+    254 <= 256) for the rest of partition 0, whose raw summary s = 10 z then passes fp16's 65504
+    (v = 10 everywhere).  The stored fp16 summary must stay finite and the output exactly 10."""
+    from elsa_amd.attention_bwd import _with_state
+
+    shape = (1, 2, 4096, 64)
+    n = shape[2]
+    describe(f"relaxed state, fp16 summary past the fp16 range {shape}")
+    q = torch.zeros(shape, dtype=torch.float16)
+    q[..., 0] = 4.0
+    k = torch.zeros(shape, dtype=torch.float16)
+    k[:, :, 64:, 0] = 4.145  # fp16(4 / 8 * log2(e)) * 4.145 = 2.989 in base 2
+    v = torch.full(shape, 10.0, dtype=torch.float16)
+    plan = forward_plan(q)
+    assert plan["partitions"] == 4 and plan["partition_len"] == 1024 and plan["block_m"] == 256, plan
+    qd, kd, vd = (x.cuda() for x in (q, k, v))
+    outs = {
+        "twopass_attention (relaxed)": elsa_amd.twopass_attention(qd, kd, vd),
+        "_with_state relaxed": _with_state(qd, kd, vd, exact_row_max=False)[0],
+        "twopass_attention_with_state (exact)": elsa_amd.twopass_attention_with_state(qd, kd, vd)[0],
+    }
+    _, m_r, z_r = _with_state(qd, kd, vd, exact_row_max=False)
+    _, m_e, z_e = elsa_amd.twopass_attention_with_state(qd, kd, vd)
+    qt, kt, vt = (x.cuda().requires_grad_() for x in (q, k, v))
+    out_t = elsa_amd.twopass_attention_train(qt, kt, vt)
+    grads = torch.autograd.grad(out_t, (qt, kt, vt), torch.ones_like(out_t))
+    torch.cuda.synchronize()
+    outs["twopass_attention_train"] = out_t.detach()
+    for name, o in outs.items():
+        assert torch.isfinite(o).all(), name
+        assert (o.float() - 10.0).abs().max().item() <= 1e-2, name
+    for g in grads:
+        assert torch.isfinite(g).all()
+    # the same log-sum-exp from either state
+    lse_r = m_r + torch.log2(z_r)
+    lse_e = m_e + torch.log2(z_e)
+    assert (lse_r - lse_e).abs().max().item() <= 1e-4
