@@ -80,7 +80,7 @@ int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
 
   const int64_t n = a->seq_len, bh = (int64_t)a->batch * a->heads, d = a->head_dim;
   const int dp = elsa::pad_head_dim(a->head_dim);
-  const int bm = elsa::phase1_block_m(a->dtype, dp, n, a->bias.ptr != nullptr);
+  const int bm = elsa::phase1_block_m(a->dtype, dp, n, bh, a->is_causal != 0, a->bias.ptr != nullptr);
   const int kt = elsa::phase1_key_tile(a->dtype, dp);
   const size_t row_bytes = 8 + (size_t)d * dtype_size(a->summary_dtype);
 

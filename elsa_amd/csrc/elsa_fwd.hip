@@ -1338,10 +1338,18 @@ static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
 // With a bias the 64-row waves hold the bias values of two row tiles and spill (252 bytes
 // per lane at D = 64), so biased sequences stay at 128 rows: B1 H8 d64 fp16 with an
 // [H, N, N] bias, forward 2K 0.068 -> 0.040 ms, 4K 0.211 -> 0.162 ms, 8K 0.688 -> 0.555 ms.
+// Causal calls whose 256-row blocks number fewer than 256 over all heads (one per CU) take
+// 128-row blocks as well: about half of their workgroups have no keys to fold and the rest
+// differ in length, so the launch lasts as long as its longest workgroups, which 128 rows
+// halve (B1 H8 d64 fp16 forward, 256 against 128 rows: 1025 tokens 0.024 -> 0.017 ms, 2K
+// 0.026 -> 0.020 ms, 4097 0.052 -> 0.044 ms, d32 2K 0.022 -> 0.016 ms; B8 H3 1025 0.026 ->
+// 0.019 ms).  Larger causal grids keep 256 (8K level; 16K 0.332 -> 0.367 ms, 32K 1.15 ->
+// 1.35 ms with 128), and so do non-causal ones (B2 H8 2K 0.035 -> 0.038 ms with 128).
 constexpr int64_t kSmallSeq = 1024;
-int phase1_block_m(int dtype, int dp, int64_t n, bool bias) {
+int phase1_block_m(int dtype, int dp, int64_t n, int64_t bh, bool causal, bool bias) {
   if (n <= 64) return 64;
   if (dtype == ELSA_F32 || dp > 64 || bias) return 128;
+  if (causal && bh * ((n + 255) / 256) < 256) return 128;
   return n <= kSmallSeq ? 128 : 256;
 }
 

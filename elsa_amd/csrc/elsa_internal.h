@@ -75,8 +75,8 @@ struct Phase2Params {
 hipError_t launch_phase1(const Phase1Params& p, int dtype, int block_m, hipStream_t stream);
 hipError_t launch_phase2(const Phase2Params& p, hipStream_t stream);
 int phase1_key_tile(int dtype, int head_dim_padded);
-// rows per Phase-1 workgroup for a sequence of n query rows
-int phase1_block_m(int dtype, int head_dim_padded, int64_t n, bool bias);
+// rows per Phase-1 workgroup for a sequence of n query rows over bh (batch, head) pairs
+int phase1_block_m(int dtype, int head_dim_padded, int64_t n, int64_t bh, bool causal, bool bias);
 int pad_head_dim(int d);
 
 struct BwdParams {

@@ -77,7 +77,7 @@ def test_plan_north_star_routing():
     (4096, _lib.ELSA_F16, 64, 0, 4, 1024),   # the ping-pong fold's partitions of >= 1024 keys
     (4096, _lib.ELSA_BF16, 64, 0, 4, 1024),
     (2048, _lib.ELSA_F16, 64, 0, 4, 512),    # 2K keeps four partitions of 512 (the 4-wave fold)
-    (4096, _lib.ELSA_F16, 64, 1, 8, 512),    # causal keeps the 4-wave fold's partitions
+    (4096, _lib.ELSA_F16, 64, 1, 4, 1024),   # causal: 128-row blocks (a short causal grid), ~1024 workgroups
     (4096, _lib.ELSA_F16, 32, 0, 8, 512),
 ])
 def test_plan_ping_pong_partitions_from_4k(n, dtype, d, causal, parts, part):
@@ -104,7 +104,18 @@ def test_plan_causal_partitions_of_a_quarter_within_2k_8k_from_8k(n, part, parts
 
 def test_plan_causal_short_partitions_round_to_the_nearest_row_block():
     rc, p = _plan(_args(n=1025, causal=1))
-    assert rc == 0 and p.block_m == 256 and p.partition_len == 512 and p.partitions == 3
+    assert rc == 0 and p.block_m == 128 and p.partition_len == 512 and p.partitions == 3
+
+
+@pytest.mark.parametrize("n,bh,bm", [(2048, (1, 8), 128), (4097, (1, 8), 128), (1025, (8, 3), 128),
+                                     (8192, (1, 8), 256), (4097, (8, 3), 256), (32768, (1, 8), 256)])
+def test_plan_causal_block_m_by_grid_size(n, bh, bm):
+    # 128-row blocks while the 256-row grid has fewer than 256 (row block, head) pairs
+    rc, p = _plan(_args(n=n, bh=bh, causal=1))
+    assert rc == 0 and p.block_m == bm
+    assert p.partitions == 1 or p.partition_len % p.block_m == 0
+    rc, p = _plan(_args(n=n, bh=bh))
+    assert rc == 0 and p.block_m == 256  # non-causal calls keep 256 rows above 1024 tokens
 
 
 @pytest.mark.parametrize("n,d", [(300, 128), (197, 64), (49, 32)])
