@@ -569,6 +569,9 @@ void bwd_dq_half_kernel(const BwdParams p) {
   constexpr bool CAN_SPLIT = RT == 1 && WAVES == 4 && (DP == 128 || (!HAS_BIAS && DP <= 64));
   const int k_lo = CAN_SPLIT ? min(k_end, wg.z * p.split_len) : 0;
   const int k_hi = CAN_SPLIT ? min(k_end, k_lo + p.split_len) : k_end;
+  // a causal key range past this row block's last row adds nothing: no partial is written, and
+  // the combine (bwd_combine_kernel, kind 1) skips the same ranges
+  if (CAN_SPLIT && p.split > 1 && p.causal && k_lo >= k_hi) return;
   // -D of this lane's row: the dP^T product starts from it and yields dP - D directly.  The
   // 16 registers per row tile of that constant would spill in the bias, D = 128 and two-tile
   // variants, which subtract D from each score instead.
@@ -919,6 +922,9 @@ static_for<0, NCH>([&](auto I) {
   const int r_lo = max(p.causal ? (wg_key0 / RTS) * RTS : 0, CAN_SPLIT ? wg.z * p.split_len : 0);
   const int r_hi = CAN_SPLIT ? min(p.N, wg.z * p.split_len + p.split_len) : p.N;
   const int ntiles = r_hi > r_lo ? (r_hi - r_lo + RTS - 1) / RTS : 0;
+  // a causal row range before this key block's first row adds nothing: no partials are written,
+  // and the combine (bwd_combine_kernel, kind 2) skips the same ranges
+  if (CAN_SPLIT && p.split > 1 && p.causal && ntiles == 0) return;
   // stage rows [t0, t0 + RTS) from LDS buffer buf into the dK / dV accumulators
   auto compute = [&](int buf, int t0) __attribute__((always_inline)) {
     if (!p.causal || t0 + RTS - 1 >= key0) {
@@ -1315,16 +1321,24 @@ int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias) {
 }
 
 // out[b, h, n, d] = scale * sum over the split ranges of part[z][b*H + h][n][d], 4 head-dim
-// elements per thread (head dims are multiples of 8); grid y picks one of up to three such sums
+// elements per thread (head dims are multiples of 8); grid y picks one of up to three such sums.
+// kind 0 sums every range.  Causal calls skip the ranges whose work-groups wrote nothing (the
+// split kernels are the 4-wave ones: 128 rows or keys per work-group):
+//   kind 1 (dQ of row n): key ranges z with z * split_len >= k_end = min(N, 128 * (n / 128 + 1));
+//   kind 2 (dK, dV of key n): row ranges z with (z + 1) * split_len <= 128 * (n / 128).
+// Every kind skips ranges that start at or past N.  Those ranges would add zeros, so the sums are
+// the same up to the sign of a zero.
 struct CombineOut {
   const float* part;
   void* out;
   int64_t os[3];
   float scale;
+  int kind;
 };
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_combine_kernel(CombineOut c0, CombineOut c1, CombineOut c2, int split,
-                                                          int64_t sstride, int H, int N, int D, int dp) {
+                                                          int split_len, int64_t sstride, int H, int N, int D,
+                                                          int dp) {
   const CombineOut& cj = blockIdx.y == 0 ? c0 : (blockIdx.y == 1 ? c1 : c2);
   const float* __restrict__ part = cj.part;
   T* __restrict__ out = static_cast<T*>(cj.out);
@@ -1335,16 +1349,24 @@ __global__ __launch_bounds__(256) void bwd_combine_kernel(CombineOut c0, Combine
   const int64_t row = i / c4;  // over B*H*N
   if (row >= sstride / dp) return;
   const int d = (int)(i - row * c4) * 4;
+  const int64_t bh = row / N, n = row - bh * N;
+  // ranges that start at or past N (split_len is rounded up to whole stages) hold nothing either
+  int z_lo = 0, z_hi = min(split, (N + split_len - 1) / split_len);
+  if (cj.kind == 1) {
+    const int k_end = min(N, 128 * ((int)n / 128 + 1));
+    z_hi = min(z_hi, (k_end + split_len - 1) / split_len);
+  } else if (cj.kind == 2) {
+    z_lo = 128 * ((int)n / 128) / split_len;  // < z_hi: 128 * (n / 128) <= n < N
+  }
   const float* src = part + row * dp + d;
-  f32x4 acc = *reinterpret_cast<const f32x4*>(src);
-  for (int z = 1; z < split; ++z) {
+  f32x4 acc = *reinterpret_cast<const f32x4*>(src + z_lo * sstride);
+  for (int z = z_lo + 1; z < z_hi; ++z) {
     const f32x4 v = *reinterpret_cast<const f32x4*>(src + z * sstride);
     acc[0] += v[0];
     acc[1] += v[1];
     acc[2] += v[2];
     acc[3] += v[3];
   }
-  const int64_t bh = row / N, n = row - bh * N;
   typedef T t4 __attribute__((ext_vector_type(4)));
   const t4 o = {static_cast<T>(acc[0] * scale), static_cast<T>(acc[1] * scale), static_cast<T>(acc[2] * scale),
                 static_cast<T>(acc[3] * scale)};
@@ -1357,7 +1379,8 @@ static hipError_t combine_launch(const BwdParams& p, const CombineOut* c, int n,
   const int64_t rows = (int64_t)p.BH * p.N;
   const int64_t threads = rows * (p.D / 4);
   hipLaunchKernelGGL(bwd_combine_kernel<T>, dim3((unsigned)((threads + 255) / 256), (unsigned)n), dim3(256), 0, st,
-                     c[0], c[n > 1 ? 1 : 0], c[n > 2 ? 2 : 0], p.split, rows * p.dp, p.H, p.N, p.D, p.dp);
+                     c[0], c[n > 1 ? 1 : 0], c[n > 2 ? 2 : 0], p.split, p.split_len, rows * p.dp, p.H, p.N, p.D,
+                     p.dp);
   return hipGetLastError();
 }
 
@@ -1387,9 +1410,10 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
         // an under-filled grid (short sequences, few heads): the key (dq) or row (dK/dV) loop cut
         // into p.split ranges over grid z, fp32 partials summed by a combine launch
         const dim3 gs(grid.x, grid.y, (unsigned)p.split);
-        const CombineOut cq{p.part, p.dq, {p.dqs[0], p.dqs[1], p.dqs[2]}, p.scale};
-        const CombineOut ck{p.part + p.part_stride, p.dk, {p.dks[0], p.dks[1], p.dks[2]}, p.scale};
-        const CombineOut cv{p.part + 2 * p.part_stride, p.dv, {p.dvs[0], p.dvs[1], p.dvs[2]}, 1.f};
+        const int kq = p.causal ? 1 : 0, kkv = p.causal ? 2 : 0;
+        const CombineOut cq{p.part, p.dq, {p.dqs[0], p.dqs[1], p.dqs[2]}, p.scale, kq};
+        const CombineOut ck{p.part + p.part_stride, p.dk, {p.dks[0], p.dks[1], p.dks[2]}, p.scale, kkv};
+        const CombineOut cv{p.part + 2 * p.part_stride, p.dv, {p.dvs[0], p.dvs[1], p.dvs[2]}, 1.f, kkv};
         if (stage < 0 || stage == 1) {
           hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, W, false>), gs, dim3(64 * W), 0, st, p);
           if ((e = hipGetLastError()) != hipSuccess) return e;

@@ -35,6 +35,8 @@ CASES = [
     ((1, 2, 197, 64), "fp16", True),
     ((1, 2, 4096, 64), "fp16", False),
     ((1, 2, 4097, 64), "fp16", True),
+    ((1, 4, 2049, 64), "fp16", True),   # split into 8 ranges of 320: the last starts past N
+    ((1, 4, 2049, 64), "fp16", False),
     ((1, 2, 300, 128), "fp16", False),
     ((1, 2, 300, 128), "fp32", True),
     ((1, 3, 197, 64), "bf16", False),
@@ -480,6 +482,38 @@ def test_backward_stages_one_by_one_are_the_whole_backward(shape, dt, causal):
         del ws
     for name, a, b in zip(("dq", "dk", "dv"), *grads):
         assert not torch.isnan(a).any() and torch.equal(a, b), name
+
+
+# The split backward's causal work-groups whose range holds nothing write no partials, and the
+# combine skips those ranges and any range that starts past N.  With the workspace filled with NaN
+# first, a partial read that no work-group wrote shows up in the gradients.
+@pytest.mark.parametrize("shape,causal", [((1, 4, 2049, 64), True), ((1, 4, 2049, 64), False),
+                                          ((1, 8, 2048, 64), True), ((8, 3, 1025, 64), True),
+                                          ((1, 2, 4097, 64), True)])
+def test_split_backward_reads_only_written_partials(shape, causal):
+    import ctypes
+    import math
+
+    from elsa_amd import _lib
+    from elsa_amd.attention import _BiasMeta
+    from elsa_amd.attention_bwd import _attach_workspace, _bwd_args
+
+    describe(f"split backward over a NaN workspace {shape} causal={causal}")
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(32)
+    q, k, v, do = (torch.randn(shape, generator=g).half().cuda() for _ in range(4))
+    out, rm, rz = elsa_amd.twopass_attention_with_state(q, k, v, is_causal=causal)
+    want = elsa_amd.twopass_attention_backward(q, k, v, out, do, is_causal=causal, row_m=rm, row_z=rz)
+    dq, dk, dv = (torch.full_like(x, float("nan")) for x in (q, k, v))
+    ba = _bwd_args(q, k, v, out, do, rm, rz, dq, dk, dv, _BiasMeta(None, 0, 0, 0, 0, False), is_causal=causal,
+                   scale=1.0 / math.sqrt(shape[-1]))
+    ws = _attach_workspace(lib, ba, q.device)
+    ws[: ws.numel() // 4 * 4].view(torch.float32).fill_(float("nan"))
+    _lib.check(lib.elsa_bwd_stage(ctypes.byref(ba), -1, _lib.stream_handle(q.device)), "elsa_bwd_stage")
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dq", "dk", "dv"), (dq, dk, dv), want):
+        assert not torch.isnan(a).any(), name
+        assert torch.equal(a, b), name
 
 
 def test_two_tile_dq_with_large_row_sums():
