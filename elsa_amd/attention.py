@@ -304,6 +304,12 @@ def _twopass_attention(q, k, v, *, bias, is_causal, block_m, block_n, q_chunk_si
     )
     if batch * heads == 0:
         return torch.empty_like(q)
+    if all(_operand(t) is t for t in (q, k, v)):
+        # operands the kernels read in place: the C++ twin of _elsa_forward (elsa_torch.cpp,
+        # attention_forward) keeps the host side of the call out of Python; same launches and bits
+        meta = _canonical_bias(bias, batch=batch, heads=heads, seq_len=seq_len, device=q.device)
+        return _lib.torch_module().attention_forward(q, k, v, meta.tensor, bool(is_causal), _lib.dtype_code(sdt),
+                                                     int(part or 0), int(qc or 0), bool(out_bnhd))
     out, *_ = _elsa_forward(q, k, v, bias=bias, is_causal=is_causal, summary_dtype=sdt, partition_len=part,
                             q_chunk=qc, want_state=False, out_bnhd=out_bnhd)
     return out

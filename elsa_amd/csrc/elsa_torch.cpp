@@ -1,4 +1,4 @@
-// PyTorch autograd functions of the training path (host code only).
+// PyTorch functions of the training path (autograd) and the inference call (host code only).
 //
 // twopass_attention_train runs through Attention (q, k, v as given), and the timm drop-ins
 // through QkvAttention (q, k, v = qkv[:, :, 0..2] of a [B, N, 3, H, D] projection).  Both
@@ -9,7 +9,9 @@
 // so that no Python runs between the launches and the backward needs no interpreter lock
 // on autograd's device thread.  They mirror _TwopassAttentionAutograd / _TwopassQkvAutograd in
 // attention_bwd.py (the Python twins, used for inputs that need a dense padded copy) and the
-// reference's _TwopassAttentionAutograd (attention_bwd.py:842-905).
+// reference's _TwopassAttentionAutograd (attention_bwd.py:842-905).  attention_forward is the
+// inference call (twopass_attention) with the same host side in C++: one planner query, the
+// workspace and elsa_fwd, without row state.
 #include <ATen/hip/HIPContext.h>
 #include <torch/extension.h>
 
@@ -77,24 +79,27 @@ struct FwdState {
   at::Tensor out, row_m, row_z;
 };
 
-// elsa_fwd with row state on [B, H, N, D] operands (any layout the ABI accepts); out is
-// written as [B, N, H, D] memory when out_bnhd, else dense.  The state is the training
-// forward's: a reference within 8 below the row maximum, z relative to it.
+// elsa_fwd on [B, H, N, D] operands (any layout the ABI accepts); out is written as
+// [B, N, H, D] memory when out_bnhd, else dense.  With want_state the row state is stored too:
+// the training forward's, a reference within 8 below the row maximum, z relative to it.
 FwdState fwd_call(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& bias, bool causal,
-                  int64_t summary_dtype, int64_t partition_len, int64_t q_chunk, bool out_bnhd) {
+                  int64_t summary_dtype, int64_t partition_len, int64_t q_chunk, bool out_bnhd,
+                  bool want_state = true) {
   const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
   FwdState st;
   st.out = out_bnhd ? at::empty({B, N, H, D}, q.options()).permute({0, 2, 1, 3}) : at::empty({B, H, N, D}, q.options());
   const auto f32 = q.options().dtype(at::kFloat);
-  st.row_m = at::empty({B * H, N}, f32);
-  st.row_z = at::empty({B * H, N}, f32);
+  if (want_state) {
+    st.row_m = at::empty({B * H, N}, f32);
+    st.row_z = at::empty({B * H, N}, f32);
+  }
   elsa_fwd_args a{};
   a.q = q.data_ptr();
   a.k = k.data_ptr();
   a.v = v.data_ptr();
   a.out = st.out.data_ptr();
-  a.row_m = st.row_m.data_ptr<float>();
-  a.row_z = st.row_z.data_ptr<float>();
+  a.row_m = want_state ? st.row_m.data_ptr<float>() : nullptr;
+  a.row_z = want_state ? st.row_z.data_ptr<float>() : nullptr;
   a.bias = bias_desc(bias);
   a.batch = static_cast<int32_t>(B);
   a.heads = static_cast<int32_t>(H);
@@ -253,12 +258,26 @@ at::Tensor attention_train(const at::Tensor& q, const at::Tensor& k, const at::T
   return Attention::apply(q, k, v, bias, causal, summary_dtype, partition_len, q_chunk, out_bnhd);
 }
 
+// The inference forward (twopass_attention, reference attention.py:239-321) on operands the ABI
+// reads in place: no row state, so the fold keeps the relaxed one.  Mirrors _elsa_forward in
+// attention.py (the Python twin, used for inputs that need a padded copy), same arguments and bits.
+at::Tensor attention_forward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                             const c10::optional<at::Tensor>& bias, bool causal, int64_t summary_dtype,
+                             int64_t partition_len, int64_t q_chunk, bool out_bnhd) {
+  TORCH_CHECK(q.dim() == 4 && q.sizes() == k.sizes() && q.sizes() == v.sizes(), "q, k, v must share one [B,H,N,D] shape");
+  check_bias_arg(bias, q);
+  const c10::DeviceGuard guard(q.device());
+  return fwd_call(q, k, v, value_or_undefined(bias), causal, summary_dtype, partition_len, q_chunk, out_bnhd, false)
+      .out;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
-  m.doc() = "C++ autograd function of the fused-qkv ELSA training path";
+  m.doc() = "C++ host side of the ELSA training (autograd) and inference calls";
   m.def("qkv_attention_train", &qkv_attention_train, "fused-qkv two-pass attention with recompute backward");
   m.def("attention_train", &attention_train, "two-pass attention on q, k, v with recompute backward");
+  m.def("attention_forward", &attention_forward, "two-pass attention forward on q, k, v (inference)");
   m.def("current_stream", [] { return reinterpret_cast<int64_t>(current_stream()); },
         "raw handle of the stream the launches go to");
   m.def("abi_version", [] { return elsa_abi_version(); });

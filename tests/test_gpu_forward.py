@@ -316,3 +316,45 @@ def test_strided_operands_read_in_place(dt, n, causal):
     shared = elsa_amd.twopass_attention(q, k1, v1, is_causal=causal)
     ref = elsa_amd.twopass_attention(q.contiguous(), k1.contiguous(), v1.contiguous(), is_causal=causal)
     assert torch.equal(shared, ref)
+
+
+@pytest.mark.parametrize("dt,shape,causal,bias,kw", [
+    ("fp16", (8, 3, 197, 64), False, False, {}),
+    ("fp16", (1, 8, 2048, 64), True, False, {}),
+    ("bf16", (2, 3, 1025, 32), False, True, {}),
+    ("fp32", (1, 2, 300, 128), True, False, {}),
+    ("fp16", (1, 4, 4096, 64), False, False, {"block_n": 1024, "q_chunk_size": 1000}),
+    ("fp16", (1, 2, 777, 64), False, False, {"summary_dtype": torch.float32}),
+])
+def test_cpp_and_python_inference_forwards_agree(dt, shape, causal, bias, kw):
+    """twopass_attention on operands read in place runs the C++ host side (attention_forward in
+    elsa_torch.cpp); _elsa_forward is its Python twin over the same C ABI: the same bits."""
+    from elsa_amd import _lib
+    from elsa_amd.attention import _elsa_forward, _resolve_forward_options
+
+    describe(f"C++ and Python inference forward {dt} {shape} causal={causal} bias={bias} {kw}")
+    g = torch.Generator().manual_seed(41)
+    q, k, v = (torch.randn(shape, generator=g).to(TORCH_DT[dt]).cuda() for _ in range(3))
+    b = torch.randn(shape[2], shape[2], generator=g).to(TORCH_DT[dt]).cuda() if bias else None
+    calls = []
+    real = _lib.torch_module().attention_forward
+
+    def spy(*a):
+        calls.append(1)
+        return real(*a)
+
+    mod = _lib.torch_module()
+    mod.attention_forward = spy
+    try:
+        got = elsa_amd.twopass_attention(q, k, v, bias=b, is_causal=causal, **kw)
+    finally:
+        mod.attention_forward = real
+    assert calls, "twopass_attention did not take the C++ host path"
+    part, qc, sdt = _resolve_forward_options(
+        q, block_m=None, block_n=kw.get("block_n"), q_chunk_size=kw.get("q_chunk_size"),
+        summary_dtype=kw.get("summary_dtype"), phase1_warps=None, phase2_warps=None, phase1_stages=None,
+        phase2_stages=None, input_precision="auto")
+    want, *_ = _elsa_forward(q, k, v, bias=b, is_causal=causal, summary_dtype=sdt, partition_len=part, q_chunk=qc,
+                             want_state=False)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
