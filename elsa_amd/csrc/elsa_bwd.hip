@@ -1395,12 +1395,44 @@ static hipError_t pre_launch(const BwdParams& p, hipStream_t st) {
 // workgroup, register budget capped for 2 waves per SIMD (measured on MI355X at
 // B1 H8 N16K d64: dq 1.36 ms / dk-dv 1.68 ms versus 2.27 / 2.76 ms with 64-wide
 // wave tiles at 1 wave per SIMD).  fp32 keeps the 32-wide kernels above.
+// Sequences of at most 64 rows at head dims up to 32 (Swin's 49-token windows): 2-wave
+// work-groups of 64 rows or keys, so that no wave of a work-group lies wholly past N (with 4
+// waves of 32, waves 2 and 3 only staged and waited).  The split backward never applies there
+// (bwd_splits).  Wider heads keep 4 waves: at D = 64 the 2-wave fp16/bf16 dK/dV kernel spills
+// (its staging share per thread doubles) and the fp32 one drops to 1 wave per SIMD.
+template <typename T, int DP, bool B>
+static hipError_t bwd_launch_short(const BwdParams& p, int stage, hipStream_t st) {
+  constexpr int W = 2;
+  const dim3 grid((p.N + 32 * W - 1) / (32 * W), p.BH);
+  hipError_t e = hipSuccess;
+  if (stage < 0 || stage == 1) {
+    if constexpr (sizeof(T) == 2) {
+      hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, 1, W, B>), grid, dim3(64 * W), 0, st, p);
+    } else {
+      hipLaunchKernelGGL((bwd_dq_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
+    }
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (stage < 0 || stage == 2) {
+    if constexpr (sizeof(T) == 2) {
+      hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, 1, W, B>), grid, dim3(64 * W), 0, st, p);
+    } else {
+      hipLaunchKernelGGL((bwd_dkdv_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
+    }
+    e = hipGetLastError();
+  }
+  return e;
+}
+
 template <typename T, int DP, bool B>
 static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
   constexpr int W = 4;
   hipError_t e = hipSuccess;
   if (stage < 0 || stage == 0) {
     if ((e = pre_launch<T>(p, st)) != hipSuccess) return e;
+  }
+  if constexpr (DP == 32) {
+    if (p.N <= 64) return stage == 0 ? e : bwd_launch_short<T, DP, B>(p, stage, st);
   }
   if constexpr (sizeof(T) == 2) {
     constexpr int R = 1;  // one 32-wide tile per wave: 2 waves per SIMD beat wider tiles at 1

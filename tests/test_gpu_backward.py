@@ -41,6 +41,9 @@ CASES = [
     ((1, 2, 300, 128), "fp32", True),
     ((1, 3, 197, 64), "bf16", False),
     ((1, 2, 90, 40), "fp32", False),
+    ((2, 3, 49, 32), "bf16", True),     # 2-wave work-groups: at most 64 rows, head dims up to 32
+    ((4, 3, 49, 24), "fp32", False),
+    ((2, 2, 33, 32), "fp16", False),
 ]
 
 
