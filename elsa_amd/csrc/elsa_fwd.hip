@@ -441,6 +441,9 @@ void phase1_half_kernel(const Phase1Params p) {
   int k_end = min(p.N, k_begin + p.part_len);
   if (p.causal) k_end = min(k_end, wg_last + 1);
   if (k_begin >= k_end) return;  // every row of this workgroup sees the identity here
+  // causal split: a partition wholly before this work-group's 512-row block is the ping-pong
+  // launch's (causal_full_row0)
+  if (p.skip_full && (wg_row0 - p.q_start) / 512 >= causal_full_row0(kb, p.part_len)) return;
 
   const int row0 = wg_row0 + wave * ROWS_W;
   const int bi = bh / p.H, hi = bh - (bh / p.H) * p.H;
@@ -707,6 +710,25 @@ void phase1_half_kernel(const Phase1Params p) {
 }
 
 // ------------------------------------------------------------------ Phase 1, ping-pong
+// The ping-pong launch of a causal split: a 1-D grid of BH * causal_full_pairs work-groups, one per
+// pair of 512-row block and partition wholly below the diagonal.  The pairs are numbered head-major,
+// then by partition, then by row block (fastest), and xcd_linear gives each XCD a contiguous range of
+// that numbering, so its resident work-groups share one (head, partition) K/V panel in its L2.
+__device__ inline WgCoord causal_full_pair(int n, int BH, int P, int part_len) {
+  const int nrb = (n + 511) / 512;
+  const int cnt = causal_full_pairs(n, P, part_len);
+  const int idx = xcd_linear();
+  const int bh = idx / cnt;
+  int rem = idx - bh * cnt;
+  for (int kb = 0; kb < P; ++kb) {
+    const int r0 = causal_full_row0(kb, part_len);
+    const int m = max(0, nrb - r0);
+    if (rem < m) return {r0 + rem, min(bh, BH - 1), kb};
+    rem -= m;
+  }
+  return {0, min(bh, BH - 1), 0};  // not reached: idx < BH * cnt
+}
+
 // The fp16/bf16 fold without bias or causal mask, with 8 waves of 64 rows per workgroup,
 // two per SIMD, in two groups (waves 0-3 and 4-7) that take turns: while one group's waves
 // run the matrix products of a stage, the other group's waves on the same SIMDs run the
@@ -724,7 +746,9 @@ void phase1_half_kernel(const Phase1Params p) {
 // from ph = 2i+2 on.
 // Measured (per-wave timestamps): the matrix phase takes about three times as long as the
 // vector phase, and the kernel is 5% faster than the two-waves-per-SIMD fold at 16K-64K keys.
-template <typename T, int DP, bool PRE, bool EXACT>
+// CF: the ping-pong launch of a causal split (causal_full_pair): every work-group's partition lies
+// wholly before its rows, so the fold needs no mask.
+template <typename T, int DP, bool PRE, bool EXACT, bool CF = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void phase1_pp_kernel(const Phase1Params p) {
   using M = Mfma<T>;
@@ -740,7 +764,12 @@ void phase1_pp_kernel(const Phase1Params p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31, g = lane >> 5;
   const int grp = wave >> 2;
-  const WgCoord wg = panel_order();
+  WgCoord wg;
+  if constexpr (CF) {
+    wg = causal_full_pair(p.N, p.BH, p.P, p.part_len);
+  } else {
+    wg = panel_order();
+  }
   const int bh = wg.y, kb = wg.z;
   const int q_end = p.q_start + p.q_len;
   const int wg_row0 = p.q_start + wg.x * BM;
@@ -1278,6 +1307,11 @@ static hipError_t launch1(const Phase1Params& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+// The causal split pays where its ping-pong launch fills whole rounds of the chip: B1 H8 d64 fp16
+// forward 32K 1.250 -> 1.205 ms, 64K 4.97 -> 4.72 ms; but 16K 0.358 -> 0.429 ms (384 ping-pong
+// work-groups, a half-empty second round), B8 H3 N16385 1.02 -> 1.08 ms, 8K 0.116 -> 0.155 ms.
+constexpr int kCausalSplitMin = 32768;
+
 template <typename T, int DP, int RT, int W, bool B>
 static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
   constexpr int BM = 32 * RT * W;
@@ -1289,6 +1323,28 @@ static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
     // 0.061 ms.  Both kernels give the same bits, so the choice never changes a result.
     const dim3 g2((p.q_len + 511) / 512, p.BH, p.P);
     const bool pv32 = std::is_same<T, f16>::value && p.s_dtype == ELSA_F32;
+    // causal split (whole-sequence causal calls from kCausalSplitMin keys): the pairs of 512-row
+    // block and partition wholly below the diagonal, three quarters of the work at P = 4, go to
+    // the ping-pong fold (no mask there), the rest to the 4-wave fold, which skips the former;
+    // both write their own summaries and Phase 2 merges them as before.  With the exact row
+    // state both folds give the same bits as the 4-wave fold alone.
+    if (p.causal && p.q_start == 0 && p.q_len == p.N && p.part_len % BM == 0 && p.part_len >= 1024 && p.P > 1 &&
+        !p.direct && !pv32 && !p.prescale_q && p.N >= kCausalSplitMin) {
+      const int pairs = p.BH * causal_full_pairs(p.N, p.P, p.part_len);
+      if (pairs > 0) {
+        if (p.exact_max) {
+          hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, true, true>), dim3(pairs), dim3(512), 0, st, p);
+        } else {
+          hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, false, true>), dim3(pairs), dim3(512), 0, st, p);
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+      }
+      Phase1Params pd = p;
+      pd.skip_full = 1;
+      hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, false, false>), grid, dim3(64 * W), 0, st, pd);
+      return hipGetLastError();
+    }
     if (!p.causal && p.part_len >= 1024 && !pv32) {
       bool done = false;
       if constexpr (std::is_same<T, f16>::value) {

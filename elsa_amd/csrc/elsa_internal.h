@@ -51,7 +51,23 @@ struct Phase1Params {
   float* row_z;
   // element strides (batch, head, row) of q, k, v and out; the head dim is contiguous
   int64_t qs[3], ks[3], vs[3], os[3];
+  // causal split (launch1h): the 4-wave fold skips the pairs of 512-row block R and partition
+  // kb that lie wholly below the diagonal (causal_full_row0), which a ping-pong launch folds
+  int skip_full;
 };
+
+// Causal split of a whole-sequence causal Phase 1: partition kb's keys all precede the rows of
+// 512-row block R (a pair the fold needs no mask for) from R = causal_full_row0(kb, part_len) on.
+__host__ __device__ inline int causal_full_row0(int kb, int part_len) {
+  return (int)(((int64_t)(kb + 1) * part_len + 511) / 512);
+}
+// Such pairs per (batch, head): sum over the partitions of the 512-row blocks from that row on.
+__host__ __device__ inline int causal_full_pairs(int n, int P, int part_len) {
+  const int nrb = (n + 511) / 512;
+  int cnt = 0;
+  for (int kb = 0; kb < P; ++kb) cnt += max(0, nrb - causal_full_row0(kb, part_len));
+  return cnt;
+}
 
 struct Phase2Params {
   const float* m_buf;

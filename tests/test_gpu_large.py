@@ -352,6 +352,51 @@ def test_q_chunked_ping_pong_fold(dt, qc):
     _check_state(torch.from_numpy(m_e[:, rows]), torch.from_numpy(z_e[:, rows]), em, ez, "row state")
 
 
+# Whole-sequence causal calls from 32K keys split Phase 1: the pairs of 512-row block and partition
+# wholly below the diagonal run in the ping-pong fold, the rest in the 4-wave fold.  With the exact
+# row state that is the 4-wave fold's result bit for bit (a q-chunked call runs it alone over the
+# same partitions); the stateless forward (relaxed state in the ping-pong pairs) against the
+# restatement at rows on every partition edge and 512-row block edge.
+SPLIT = [((1, 4, 32768, 64), "fp16"), ((1, 2, 33000, 64), "bf16")]
+
+
+@pytest.mark.parametrize("shape,dt", SPLIT, ids=[f"{s[2]}-{d}" for s, d in SPLIT])
+def test_causal_split_fold(shape, dt):
+    from elsa_amd.attention_bwd import _with_state
+
+    b, h, n, d = shape
+    describe(f"causal split fold {shape} {dt}")
+    q, k, v, _ = _draw(shape, dt, seed=n)
+    plan = forward_plan(q, is_causal=True)
+    assert plan["partitions"] > 1 and plan["partition_len"] % 256 == 0 and plan["block_m"] == 256, plan
+    bn = plan["partition_len"]
+    qd, kd, vd = (x.cuda() for x in (q, k, v))
+    out_s, m_s, z_s = elsa_amd.twopass_attention_with_state(qd, kd, vd, is_causal=True)
+    out_c, m_c, z_c = elsa_amd.twopass_attention_with_state(qd, kd, vd, is_causal=True, block_n=bn,
+                                                            q_chunk_size=n // 2 // 256 * 256)
+    out_r, m_r, z_r = _with_state(qd, kd, vd, is_causal=True, exact_row_max=False)
+    out_i = elsa_amd.twopass_attention(qd, kd, vd, is_causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out_s, out_c) and torch.equal(m_s, m_c) and torch.equal(z_s, z_c)
+    assert torch.equal(out_i, out_r)
+    # the relaxed state: a reference within 8 below the exact maximum, the same log-sum-exp
+    m_e, z_e, m_r, z_r = (_np(t.cpu()) for t in (m_s, z_s, m_r, z_r))
+    assert (m_r <= m_e + 1e-5 * np.maximum(1.0, np.abs(m_e))).all() and (m_r >= m_e - 8.0 - 1e-5).all()
+    lse_e, lse_r = m_e + np.log2(z_e), m_r + np.log2(z_r)
+    assert np.abs(lse_r - lse_e).max() <= 2e-5 * max(1.0, np.abs(lse_e).max())
+    part, micro = O.reference_routing(n, d, dt, training=False, is_causal=True)
+    edges = [j * bn + o for j in range(1, plan["partitions"]) for o in (-1, 0, 1)]
+    edges += [r + o for r in range(512, n, 512) for o in (-1, 0)][::7]
+    rows = _rows(n, 24, seed=n + 7, extra=edges)
+    ro, _, _ = T.forward(q, k, v, is_causal=True, part_len=part, micro=micro, dtype=dt, rows=rows)
+    eo, em, ez = T.exact_forward(q, k, v, is_causal=True, rows=rows)
+    for name, o in (("out (relaxed state)", out_i), ("out (exact state)", out_s)):
+        info = assert_parity(_np(o.float().cpu()[:, :, rows]), _np(eo), _np(ro), FWD_TOL[dt], name, dt,
+                             plain=_plain(n, dt, "out", True))
+        describe(f"  {name} rows {info}")
+    _check_state(torch.from_numpy(m_e[:, rows]), torch.from_numpy(z_e[:, rows]), em, ez, "row state")
+
+
 # The backward kernels alone, at the reference's own forward result: out and (row_m, row_z) from
 # the restatement of the reference's forward, then this build's backward against the restatement
 # of the reference's backward from the same out and state.  What is left is the backward's own
