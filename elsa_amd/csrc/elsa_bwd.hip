@@ -794,7 +794,9 @@ static_for<0, NCH>([&](auto I) {
 
 // 2 waves per SIMD up to D = 64; at D = 128 the dK/dV accumulators and the wave's K/V
 // fragments alone need more than the 256 registers of that budget, so 1 wave per SIMD
-template <typename T, int DP, int KRT, int WAVES, bool HAS_BIAS>
+// LD (8 waves, D = 64, no bias): the Q and dO stage tiles go straight from global memory into LDS
+// (buffer_load_dwordx4 ... lds, one stage ahead) instead of through staging registers.
+template <typename T, int DP, int KRT, int WAVES, bool HAS_BIAS, bool LD = false>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(DP >= 128 ? 1 : 2, 2)))
 void bwd_dkdv_half_kernel(const BwdParams p) {
   using M = Mfma<T>;
@@ -809,8 +811,14 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
   constexpr int NT = 64 * WAVES, KEYS_W = 32 * KRT, BN = KEYS_W * WAVES;
   static_assert((RTS * CPR) % NT == 0, "staging must divide evenly");
   constexpr int NCH = RTS * CPR / NT;
-  __shared__ __attribute__((aligned(16))) T Qs[2][RTS * KS];
-  __shared__ __attribute__((aligned(16))) T Gs[2][RTS * KS];
+  static_assert(!LD || (WAVES == 8 && KRT == 1 && DP == 64 && !HAS_BIAS && Tile::SWZ && NCH == 2),
+                "LDS-direct staging: the 8-wave D = 64 kernel");
+  // LD: one array per buffer, so that the compiler sees the loads into one buffer leave the other
+  // one's reads alone (with one two-buffer array it waited for them before every stage's reads)
+  __shared__ __attribute__((aligned(16))) T Qs[LD ? 1 : 2][RTS * KS];
+  __shared__ __attribute__((aligned(16))) T Gs[LD ? 1 : 2][RTS * KS];
+  __shared__ __attribute__((aligned(16))) T Qs1[LD ? RTS * KS : 1];
+  __shared__ __attribute__((aligned(16))) T Gs1[LD ? RTS * KS : 1];
   __shared__ __attribute__((aligned(16))) float lse_s[2][RTS];
   __shared__ __attribute__((aligned(16))) float ndd_s[2][RTS];  // -D of the stage's rows
 
@@ -876,9 +884,49 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
     goff[i] = (uint32_t)r * (uint32_t)p.gs[2] + (uint32_t)d0;
   });
   // staging registers: set S holds one stage (RTS rows) on its way from global memory to LDS
-  Chunk16 qreg[2][NCH], greg[2][NCH];
+  Chunk16 qreg[LD ? 1 : 2][LD ? 1 : NCH], greg[LD ? 1 : 2][LD ? 1 : NCH];
   float lreg[2] = {0.f, 0.f}, dreg[2] = {0.f, 0.f};
+  // LD: lane l of wave w fills the 16 bytes at LDS byte 16 (64 w + 512 i + l) of a stage tile for
+  // i = 0, 1: row 8 w + 64 i + l / 8 of the stage, swizzle slot l % 8, which holds chunk
+  // (l % 8) ^ lds_swz(row) of that row.  Rows past N read as zeros: the buffer range ends at row N
+  // (the launcher checks that N rows of Q and of dO span less than 2^31 bytes).
+  uint32_t ldq[LD ? NCH : 1], ldg[LD ? NCH : 1];
+  const uint32_t qrb = (uint32_t)p.qs[2] * (uint32_t)sizeof(T), grb = (uint32_t)p.gs[2] * (uint32_t)sizeof(T);
+  const auto rq = make_rsrc(Q, LD ? (uint32_t)p.N * qrb : 0u);
+  const auto rg = make_rsrc(dO, LD ? (uint32_t)p.N * grb : 0u);
+  if constexpr (LD) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int r = 8 * wave + 64 * i + (lane >> 3);
+      const uint32_t ch = (uint32_t)((lane & 7) ^ lds_swz(r));
+      ldq[i] = (uint32_t)r * qrb + ch * 16u;
+      ldg[i] = (uint32_t)r * grb + ch * 16u;
+    }
+  }
+  auto ldload = [&](int t0, T* qdst, T* gdst) {
+    if constexpr (LD) {
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        buffer_load16_lds(rq, qdst + (64 * wave + 512 * i) * 8, ldq[i] + (uint32_t)t0 * qrb);
+        buffer_load16_lds(rg, gdst + (64 * wave + 512 * i) * 8, ldg[i] + (uint32_t)t0 * grb);
+      }
+      // rows past N: LSE2 = +inf makes their p exactly 0.  D is negated at the store, so that no
+      // instruction here waits for these loads (and with them for the LDS loads issued before)
+      if (tid < RTS) {
+        const int ra = t0 + tid;
+        lreg[0] = ra < p.N ? p.lse_row[(int64_t)bh * p.N + ra] : __builtin_huge_valf();
+        dreg[0] = ra < p.N ? p.d_row[(int64_t)bh * p.N + ra] : 0.f;
+      }
+    }
+  };
+  auto ldstore = [&](int buf) {
+    if (tid < RTS) {
+      lse_s[buf][tid] = lreg[0];
+      ndd_s[buf][tid] = -dreg[0];
+    }
+  };
   auto gload = [&](int t0, auto SET) {
+    if constexpr (LD) return;
     constexpr int S = decltype(SET)::value;
     const T* qt = Q + (int64_t)t0 * p.qs[2];
     const T* gt = dO + (int64_t)t0 * p.gs[2];
@@ -901,6 +949,7 @@ static_for<0, NCH>([&](auto I) {
     }
   };
   auto sstore = [&](int buf, auto SET) {
+    if constexpr (LD) return;
     constexpr int S = decltype(SET)::value;
 static_for<0, NCH>([&](auto I) {
       constexpr int i = decltype(I)::value;
@@ -926,10 +975,8 @@ static_for<0, NCH>([&](auto I) {
   // and the combine (bwd_combine_kernel, kind 2) skips the same ranges
   if (CAN_SPLIT && p.split > 1 && p.causal && ntiles == 0) return;
   // stage rows [t0, t0 + RTS) from LDS buffer buf into the dK / dV accumulators
-  auto compute = [&](int buf, int t0) __attribute__((always_inline)) {
+  auto compute = [&](int buf, int t0, const T* qs, const T* gs) __attribute__((always_inline)) {
     if (!p.causal || t0 + RTS - 1 >= key0) {
-      const T* qs = Qs[buf];
-      const T* gs = Gs[buf];
 #pragma unroll
       for (int sub = 0; sub < RTS / 32; ++sub) {
         F qa[NKK], ga[NKK];
@@ -1038,6 +1085,31 @@ static_for<0, NCH>([&](auto I) {
   };
   const auto S0 = std::integral_constant<int, 0>{};
   const auto S1 = std::integral_constant<int, 1>{};
+  if constexpr (LD) {
+    // stage it + 1 goes into the other LDS buffer while stage it computes (that buffer was last
+    // read by stage it - 1, before the barrier that ended it); all loads land before the barrier
+    if (ntiles > 0) {
+      ldload(r_lo, Qs[0], Gs[0]);
+      ldstore(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int it = 0; it < ntiles; it += 2) {
+      const int t0 = r_lo + it * RTS;
+      if (it + 1 < ntiles) ldload(t0 + RTS, Qs1, Gs1);
+      compute(0, t0, Qs[0], Gs[0]);
+      if (it + 1 < ntiles) ldstore(1);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (it + 1 < ntiles) {
+        if (it + 2 < ntiles) ldload(t0 + 2 * RTS, Qs[0], Gs[0]);
+        compute(1, t0 + RTS, Qs1, Gs1);
+        if (it + 2 < ntiles) ldstore(0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+      }
+    }
+  } else {
   // global loads two stages ahead: stage it + 2 goes into the register set that stage it
   // left, while stage it + 1 waits in the other one for the end of this stage
   gload(r_lo, S0);
@@ -1048,13 +1120,14 @@ static_for<0, NCH>([&](auto I) {
     const int buf = it & 1;
     const int t0 = r_lo + it * RTS;
     if (it + 2 < ntiles) gload(t0 + 2 * RTS, FREE);
-    compute(buf, t0);
+    compute(buf, t0, Qs[buf], Gs[buf]);
     if (it + 1 < ntiles) sstore(buf ^ 1, NEXT);
     __syncthreads();
   };
   for (int it = 0; it < ntiles; it += 2) {
     step(it, S1, S0);
     if (it + 1 < ntiles) step(it + 1, S0, S1);
+  }
   }
 #pragma unroll
   for (int kt = 0; kt < KRT; ++kt) {
@@ -1510,7 +1583,19 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
       if constexpr (DP == 64) {
         const dim3 g8((p.N + 255) / 256, p.BH);
         if ((int64_t)g8.x * g8.y >= 512) {
-          hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, 8, B>), g8, dim3(512), 0, st, p);
+          // LDS-direct staging where every head dim chunk is data (D = 64) and the buffer ranges of
+          // N rows of Q and dO stay below 2^31 bytes
+          const bool ld = !B && p.D == 64 && (int64_t)p.N * p.qs[2] * (int64_t)sizeof(T) < (int64_t(1) << 31) &&
+                          (int64_t)p.N * p.gs[2] * (int64_t)sizeof(T) < (int64_t(1) << 31);
+          if constexpr (!B) {
+            if (ld) {
+              hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, 8, false, true>), g8, dim3(512), 0, st, p);
+            } else {
+              hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, 8, B>), g8, dim3(512), 0, st, p);
+            }
+          } else {
+            hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, 8, B>), g8, dim3(512), 0, st, p);
+          }
           w8 = true;
         }
       }

@@ -139,6 +139,11 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t by
 __device__ inline Chunk16 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(Chunk16, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
+// 16 bytes per lane from a buffer straight into LDS (buffer_load_dwordx4 ... lds): lane i's bytes
+// land at lds + 16 i (lds is wave-uniform: it goes to M0); offsets past the buffer range read zeros
+__device__ inline void buffer_load16_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
 
 // acc + a + b with an fp32 accumulator (v_dot2_f32_f16 / v_dot2_f32_bf16 against (1, 1)).
 __device__ inline float sum2(f16 a, f16 b, float acc) {
