@@ -509,7 +509,9 @@ __device__ inline typename Mfma<T>::frag tr_frag_at(const T* tile, int r0, int c
 }
 
 
-template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS>
+// LD (the two-tile 8-wave kernel at D = 64): the K and V stage tiles go straight from global memory
+// into LDS (buffer_load_dwordx4 ... lds, one stage ahead) instead of through staging registers.
+template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS, bool LD = false>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void bwd_dq_half_kernel(const BwdParams p) {
   using M = Mfma<T>;
@@ -522,8 +524,13 @@ void bwd_dq_half_kernel(const BwdParams p) {
   constexpr int NT = 64 * WAVES, ROWS_W = 32 * RT, BM = ROWS_W * WAVES;
   static_assert((KT * CPR) % NT == 0, "staging must divide evenly");
   constexpr int NCH = KT * CPR / NT;
-  __shared__ __attribute__((aligned(16))) T Ks[2][KT * KS];
-  __shared__ __attribute__((aligned(16))) T Vs[2][KT * KS];
+  static_assert(!LD || (RT == 2 && WAVES == 8 && DP == 64 && !HAS_BIAS && KT == 64 && KS == 72),
+                "LDS-direct staging: the two-tile 8-wave D = 64 kernel, padded 144-byte rows");
+  // LD: one array per buffer (see bwd_dkdv_half_kernel)
+  __shared__ __attribute__((aligned(16))) T Ks[LD ? 1 : 2][KT * KS];
+  __shared__ __attribute__((aligned(16))) T Vs[LD ? 1 : 2][KT * KS];
+  __shared__ __attribute__((aligned(16))) T Ks1[LD ? KT * KS : 1];
+  __shared__ __attribute__((aligned(16))) T Vs1[LD ? KT * KS : 1];
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
@@ -617,8 +624,37 @@ void bwd_dq_half_kernel(const BwdParams p) {
   const int32_t koff0 = (tid / CPR) * (int32_t)p.ks[2] + (tid % CPR) * 8;
   const int32_t voff0 = (tid / CPR) * (int32_t)p.vs[2] + (tid % CPR) * 8;
   // staging registers: set S holds one 64-key stage on its way from global memory to LDS
-  Chunk16 kreg[2][NCH], vreg[2][NCH];
+  Chunk16 kreg[LD ? 1 : 2][LD ? 1 : NCH], vreg[LD ? 1 : 2][LD ? 1 : NCH];
+  // LD: a stage tile is 64 padded rows of 9 16-byte slots (8 of data, 1 of padding), 576 slots; the
+  // lanes of wave w fill slots 64 (w + 8 j) .. + 63 (j = 0, and j = 1 for wave 0 only): slot f holds
+  // chunk f % 9 of row f / 9, and a padding slot (f % 9 == 8, never read) takes that row's chunk 0.
+  // Keys past N read as zeros: the buffer range ends at row N (the launcher checks that N rows of
+  // K and of V span less than 2^31 bytes).
+  uint32_t ldk[LD ? 2 : 1], ldv[LD ? 2 : 1];
+  const uint32_t krb = (uint32_t)p.ks[2] * (uint32_t)sizeof(T), vrb = (uint32_t)p.vs[2] * (uint32_t)sizeof(T);
+  const auto rk = make_rsrc(K, LD ? (uint32_t)p.N * krb : 0u);
+  const auto rv = make_rsrc(V, LD ? (uint32_t)p.N * vrb : 0u);
+  if constexpr (LD) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int f = 64 * (wave + 8 * j) + lane;
+      const int r = f / 9, ch = f % 9 == 8 ? 0 : f % 9;
+      ldk[j] = (uint32_t)r * krb + (uint32_t)ch * 16u;
+      ldv[j] = (uint32_t)r * vrb + (uint32_t)ch * 16u;
+    }
+  }
+  auto ldload = [&](int t0, T* kdst, T* vdst) {
+    if constexpr (LD) {
+      buffer_load16_lds(rk, kdst + 64 * wave * 8, ldk[0] + (uint32_t)t0 * krb);
+      buffer_load16_lds(rv, vdst + 64 * wave * 8, ldv[0] + (uint32_t)t0 * vrb);
+      if (wave == 0) {
+        buffer_load16_lds(rk, kdst + 512 * 8, ldk[1] + (uint32_t)t0 * krb);
+        buffer_load16_lds(rv, vdst + 512 * 8, ldv[1] + (uint32_t)t0 * vrb);
+      }
+    }
+  };
   auto gload = [&](int t0, auto SET) {
+    if constexpr (LD) return;
     constexpr int S = decltype(SET)::value;
     const T* kt = K + (int64_t)t0 * p.ks[2];
     const T* vt = V + (int64_t)t0 * p.vs[2];
@@ -636,6 +672,7 @@ static_for<0, NCH>([&](auto I) {
     });
   };
   auto sstore = [&](int buf, auto SET) {
+    if constexpr (LD) return;
     constexpr int S = decltype(SET)::value;
 static_for<0, NCH>([&](auto I) {
       constexpr int i = decltype(I)::value;
@@ -654,10 +691,8 @@ static_for<0, NCH>([&](auto I) {
 
   const int ntiles = (k_hi - k_lo + KT - 1) / KT;
   // stage keys [t0, t0 + KT) from LDS buffer buf into the dQ accumulators
-  auto compute = [&](int buf, int t0) __attribute__((always_inline)) {
+  auto compute = [&](int t0, const T* ks, const T* vs) __attribute__((always_inline)) {
     if (!p.causal || t0 <= row0 + ROWS_W - 1) {
-      const T* ks = Ks[buf];
-      const T* vs = Vs[buf];
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         F kf[NKK], vf[NKK];
@@ -738,13 +773,32 @@ static_for<0, NCH>([&](auto I) {
       const int buf = it & 1;
       const int t0 = k_lo + it * KT;
       if (it + 2 < ntiles) gload(t0 + 2 * KT, FREE);
-      compute(buf, t0);
+      compute(t0, Ks[buf], Vs[buf]);
       if (it + 1 < ntiles) sstore(buf ^ 1, NEXT);
       __syncthreads();
     };
     for (int it = 0; it < ntiles; it += 2) {
       step(it, S1, S0);
       if (it + 1 < ntiles) step(it + 1, S0, S1);
+    }
+  } else if constexpr (LD) {
+    // stage it + 1 goes into the other LDS buffer while stage it computes; all loads land before
+    // the barrier that ends the stage
+    if (ntiles > 0) ldload(k_lo, Ks[0], Vs[0]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int it = 0; it < ntiles; it += 2) {
+      const int t0 = k_lo + it * KT;
+      if (it + 1 < ntiles) ldload(t0 + KT, Ks1, Vs1);
+      compute(t0, Ks[0], Vs[0]);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (it + 1 < ntiles) {
+        if (it + 2 < ntiles) ldload(t0 + 2 * KT, Ks[0], Vs[0]);
+        compute(t0 + KT, Ks1, Vs1);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+      }
     }
   } else {
     gload(k_lo, S0);
@@ -755,7 +809,7 @@ static_for<0, NCH>([&](auto I) {
       const int t0 = k_lo + it * KT;
       const bool has_next = it + 1 < ntiles;
       if (has_next) gload(t0 + KT, S0);
-      compute(buf, t0);
+      compute(t0, Ks[buf], Vs[buf]);
       if (has_next) sstore(buf ^ 1, S0);
       __syncthreads();
     }
@@ -1555,7 +1609,15 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
         if constexpr (DP == 64) {
           const dim3 grid8((p.N + 511) / 512, p.BH);
           if (wide && (int64_t)grid8.x * grid8.y >= 256) {
-            hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, 2, 8, false>), grid8, dim3(512), 0, st, p);
+            // LDS-direct staging where every head dim chunk is data (D = 64) and the buffer ranges of
+            // N rows of K and V stay below 2^31 bytes
+            const bool ld = p.D == 64 && (int64_t)p.N * p.ks[2] * (int64_t)sizeof(T) < (int64_t(1) << 31) &&
+                            (int64_t)p.N * p.vs[2] * (int64_t)sizeof(T) < (int64_t(1) << 31);
+            if (ld) {
+              hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, 2, 8, false, true>), grid8, dim3(512), 0, st, p);
+            } else {
+              hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, 2, 8, false>), grid8, dim3(512), 0, st, p);
+            }
             w8 = true;
           }
         }
