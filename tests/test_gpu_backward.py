@@ -240,16 +240,20 @@ def test_dbias_split_reduction_matches_unsplit_and_closed_form(bias_shape):
                                atol=1e-6 * (shape[0] * shape[1]) ** 0.5)
 
 
-@pytest.mark.parametrize("dt,n,causal,d", [("fp16", 197, False, 64), ("bf16", 1025, True, 64), ("fp32", 300, False, 64),
-                                           ("fp16", 4097, True, 64), ("fp16", 49, False, 32), ("fp16", 300, False, 128)])
-def test_strided_backward_is_bitwise_the_dense_one(dt, n, causal, d):
+@pytest.mark.parametrize("dt,n,causal,d,bh", [("fp16", 197, False, 64, (2, 3)), ("bf16", 1025, True, 64, (2, 3)),
+                                              ("fp32", 300, False, 64, (2, 3)), ("fp16", 4097, True, 64, (2, 3)),
+                                              ("fp16", 49, False, 32, (2, 3)), ("fp16", 300, False, 128, (2, 3)),
+                                              # the 8-wave dq and dK/dV kernels, which load Q/dO and K/V
+                                              # straight into LDS through the strided rows
+                                              ("fp16", 16384, False, 64, (1, 8)), ("bf16", 16384, True, 64, (1, 8))])
+def test_strided_backward_is_bitwise_the_dense_one(dt, n, causal, d, bh):
     """q, k, v as views of a fused [B,N,3,H,D] projection, out and dO as [B,N,H,D] memory,
     and dq, dk, dv written into one fused [B,N,3,H,D] gradient: the same bits as the
     backward on dense copies.  The kernels read and write through the layouts, no copy."""
     from elsa_amd.attention import _BiasMeta
     from elsa_amd.attention_bwd import _backward, _with_state
 
-    b, h = 2, 3
+    b, h = bh
     describe(f"strided backward {dt} n={n} causal={causal} d={d}")
     g = torch.Generator().manual_seed(4242 + n)
     qkv = (torch.randn((b, n, 3, h, d), generator=g) * 0.5).to(TORCH_DT[dt]).cuda()
