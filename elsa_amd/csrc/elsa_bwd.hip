@@ -1595,7 +1595,7 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
     }
     if (stage < 0 || stage == 1) {
       // dq with two 32-row tiles per wave: each K/V fragment read from LDS feeds both tiles,
-      // halving the LDS reads per MFMA.  Non-causal, unbiased, D <= 64, and only where the grid
+      // halving the LDS reads per MFMA.  Unbiased, D <= 64 (causal: below), and only where the grid
       // still puts two 256-row work-groups on every CU.  B1 H8 d64 16K: fp16 0.875 -> 0.814 ms, bf16
       // 0.841 -> 0.768 ms; causal 16K 0.479 against 0.510 ms and 4K (128 work-groups) 0.074 against
       // 0.111 ms stay on the 32-row kernel.  At D = 64, 8-wave work-groups of 512 rows (one per CU,
@@ -1604,11 +1604,17 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
       const dim3 grid2((p.N + 255) / 256, p.BH);
       bool wide = false;
       if constexpr (DP <= 64 && !B) {
-        wide = !p.causal && (int64_t)grid2.x * grid2.y >= 512;
+        // causal calls take the two-tile kernel where its 512-row work-groups come in whole pairs of
+        // rounds (a multiple of 512) over heads of at least 32 row blocks, so that the heaviest-first
+        // order balances: dq causal 32K 1.616 -> 1.514 ms, 64K 6.35 -> 5.89 ms, B1 H16 16K 0.829 ->
+        // 0.787 ms, B2 H8 16K bf16 0.778 -> 0.738 ms; one round (B1 H8 16K, 256 work-groups) took
+        // 0.427 -> 0.605 ms, B4 H8 8K 0.457 -> 0.555 ms and B8 H3 N16385 (792) 1.25 -> 1.37 ms
+        const dim3 grid8((p.N + 511) / 512, p.BH);
+        const int64_t n8 = (int64_t)grid8.x * grid8.y;
+        wide = (int64_t)grid2.x * grid2.y >= 512 && (!p.causal || (DP == 64 && p.N >= 16384 && n8 % 512 == 0));
         bool w8 = false;
         if constexpr (DP == 64) {
-          const dim3 grid8((p.N + 511) / 512, p.BH);
-          if (wide && (int64_t)grid8.x * grid8.y >= 256) {
+          if (wide && n8 >= 256) {
             // LDS-direct staging where every head dim chunk is data (D = 64) and the buffer ranges of
             // N rows of K and V stay below 2^31 bytes
             const bool ld = p.D == 64 && (int64_t)p.N * p.ks[2] * (int64_t)sizeof(T) < (int64_t(1) << 31) &&
