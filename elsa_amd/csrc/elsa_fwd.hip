@@ -404,7 +404,7 @@ constexpr float kLazySum = 256.0f;  // 2^kLazyTau
 //
 // 2 waves per SIMD, except the 1- and 2-wave variants at D >= 64 (sequences of at most 64
 // keys): their register staging of a whole 64-key stage does not fit that budget.
-template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS, bool PRE, bool PV32 = false>
+template <typename T, int DP, int RT, int WAVES, bool HAS_BIAS, bool PRE, bool PV32 = false, bool LD = false>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu((WAVES <= 2 && DP >= 64) ? 1 : 2, 2)))
 void phase1_half_kernel(const Phase1Params p) {
   static_assert(!(PRE && HAS_BIAS), "the prescaled fold has no bias");
@@ -423,8 +423,14 @@ void phase1_half_kernel(const Phase1Params p) {
   static_assert((KT * CPR) % NT == 0, "staging must divide evenly");
   constexpr int NCH = KT * CPR / NT;
 
-  __shared__ __attribute__((aligned(16))) T Ks[2][KT * KS];
-  __shared__ __attribute__((aligned(16))) T Vs[2][KT * KS];
+  static_assert(!LD || (WAVES == 4 && DP == 64 && !HAS_BIAS && !PV32 && KS == 72),
+                "LDS-direct staging: the 4-wave D = 64 fold, padded 144-byte rows");
+  // LD: one array per buffer, so that the compiler sees the loads into one buffer leave the other
+  // one's reads alone
+  __shared__ __attribute__((aligned(16))) T Ks[LD ? 1 : 2][KT * KS];
+  __shared__ __attribute__((aligned(16))) T Vs[LD ? 1 : 2][KT * KS];
+  __shared__ __attribute__((aligned(16))) T Ks1[LD ? KT * KS : 1];
+  __shared__ __attribute__((aligned(16))) T Vs1[LD ? KT * KS : 1];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31, g = lane >> 5;
@@ -486,8 +492,38 @@ void phase1_half_kernel(const Phase1Params p) {
     kvoff[i] = d0 < p.D ? (uint32_t)key * krs + dofs : kBufferOff;
     vvoff[i] = d0 < p.D ? (uint32_t)key * vrs + dofs : kBufferOff;
   });
-  Chunk16 kreg[NCH], vreg[NCH];
+  Chunk16 kreg[LD ? 1 : NCH], vreg[LD ? 1 : NCH];
+  // LD: K and V stage tiles straight into LDS (buffer_load_dwordx4 ... lds, one stage ahead).  A
+  // tile is 64 padded rows of 9 16-byte slots (8 of data, 1 of padding, never read), 576 slots; the
+  // lanes of wave w fill slots 64 (w + 4 j) .. + 63 (j = 0, 1, and j = 2 for wave 0 only): slot f
+  // holds chunk f % 9 of key row f / 9, the padding slot that row's chunk 0.  Keys past k_end read
+  // as zeros from the buffer range (LD runs only at D = 64, where every chunk is data).
+  uint32_t ldk[LD ? 3 : 1], ldv[LD ? 3 : 1];
+  if constexpr (LD) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int f = 64 * (wave + 4 * j) + lane;
+      const int r = f / 9, ch = f % 9 == 8 ? 0 : f % 9;
+      ldk[j] = (uint32_t)r * krs + (uint32_t)ch * 16u;
+      ldv[j] = (uint32_t)r * vrs + (uint32_t)ch * 16u;
+    }
+  }
+  auto ldload = [&](int t0, T* kdst, T* vdst) {
+    if constexpr (LD) {
+      const uint32_t kt = (uint32_t)(t0 - k_begin);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        buffer_load16_lds(rk, kdst + 64 * (wave + 4 * j) * 8, ldk[j] + kt * krs);
+        buffer_load16_lds(rv, vdst + 64 * (wave + 4 * j) * 8, ldv[j] + kt * vrs);
+      }
+      if (wave == 0) {
+        buffer_load16_lds(rk, kdst + 512 * 8, ldk[2] + kt * krs);
+        buffer_load16_lds(rv, vdst + 512 * 8, ldv[2] + kt * vrs);
+      }
+    }
+  };
   auto gload = [&](int t0) {
+    if constexpr (LD) return;
     // the stage offset goes into the VGPR offset, so that the range check sees it
     const uint32_t kt = (uint32_t)(t0 - k_begin);
     static_for<0, NCH>([&](auto I) {
@@ -497,6 +533,7 @@ void phase1_half_kernel(const Phase1Params p) {
     });
   };
   auto sstore = [&](int buf) {
+    if constexpr (LD) return;
     static_for<0, NCH>([&](auto I) {
       constexpr int i = decltype(I)::value;
       const int ci = tid + i * NT;
@@ -524,20 +561,11 @@ void phase1_half_kernel(const Phase1Params p) {
 #pragma unroll
   for (int rt = 0; rt < (PRE ? RT : 1); ++rt) negref[rt] = f32x16{};
 
-  gload(k_begin);
-  sstore(0);
-  __syncthreads();
-
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
-    const int t0 = k_begin + it * KT;
-    const bool has_next = it + 1 < ntiles;
-    if (has_next) gload(t0 + KT);
+  // stage keys [t0, t0 + KT) from the LDS tiles ks, vs
+  auto stage = [&](int t0, const T* ks, const T* vs) __attribute__((always_inline)) {
     // a causal wave whose rows all precede this stage has nothing to add
     const bool active = !p.causal || t0 <= row0 + ROWS_W - 1;
     if (active) {
-      const T* ks = Ks[buf];
-      const T* vs = Vs[buf];
       f32x16 s[RT][NSUB];
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub) {
@@ -681,8 +709,39 @@ void phase1_half_kernel(const Phase1Params p) {
           }
         }
     }
-    if (has_next) sstore(buf ^ 1);
+  };
+  if constexpr (LD) {
+    // stage it + 1 goes into the other LDS buffer while stage it computes; all loads land before
+    // the barrier that ends the stage
+    ldload(k_begin, Ks[0], Vs[0]);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    for (int it = 0; it < ntiles; it += 2) {
+      const int t0 = k_begin + it * KT;
+      if (it + 1 < ntiles) ldload(t0 + KT, Ks1, Vs1);
+      stage(t0, Ks[0], Vs[0]);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (it + 1 < ntiles) {
+        if (it + 2 < ntiles) ldload(t0 + 2 * KT, Ks[0], Vs[0]);
+        stage(t0 + KT, Ks1, Vs1);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+      }
+    }
+  } else {
+    gload(k_begin);
+    sstore(0);
+    __syncthreads();
+    for (int it = 0; it < ntiles; ++it) {
+      const int buf = it & 1;
+      const int t0 = k_begin + it * KT;
+      const bool has_next = it + 1 < ntiles;
+      if (has_next) gload(t0 + KT);
+      stage(t0, Ks[buf], Vs[buf]);
+      if (has_next) sstore(buf ^ 1);
+      __syncthreads();
+    }
   }
 
 #pragma unroll
@@ -1367,9 +1426,18 @@ static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
       return hipGetLastError();
     }
   }
+  // the 4-wave one-tile D = 64 fold (128-row blocks) stages K and V straight into LDS (LD): causal
+  // B1 H8 Phase 1 at 4097 tokens 0.0377 -> 0.0356 ms, B8 H3 N1025 0.0143 -> 0.0140 ms, 2K 0.0145 ->
+  // 0.0143 ms.  The two-tile fold keeps registers: with LD its unrolled loop took 256 VGPRs against
+  // 238, and causal 8K-32K and bf16 2K ran 0.5-5% slower.
+  constexpr bool LDOK = !B && DP == 64 && W == 4 && RT == 1;
   if constexpr (!B && DP == 64 && std::is_same<T, f16>::value) {
     if (p.prescale_q) {
-      hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, false, true>), grid, dim3(64 * W), 0, st, p);
+      if (LDOK && p.D == 64) {
+        hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, false, true, false, LDOK>), grid, dim3(64 * W), 0, st, p);
+      } else {
+        hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, false, true>), grid, dim3(64 * W), 0, st, p);
+      }
       return hipGetLastError();
     }
   }
@@ -1379,7 +1447,11 @@ static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, B, false>), grid, dim3(64 * W), 0, st, p);
+  if (LDOK && p.D == 64) {
+    hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, B, false, false, LDOK>), grid, dim3(64 * W), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((phase1_half_kernel<T, DP, RT, W, B, false>), grid, dim3(64 * W), 0, st, p);
+  }
   return hipGetLastError();
 }
 
