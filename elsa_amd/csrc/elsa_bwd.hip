@@ -524,8 +524,8 @@ void bwd_dq_half_kernel(const BwdParams p) {
   constexpr int NT = 64 * WAVES, ROWS_W = 32 * RT, BM = ROWS_W * WAVES;
   static_assert((KT * CPR) % NT == 0, "staging must divide evenly");
   constexpr int NCH = KT * CPR / NT;
-  static_assert(!LD || (RT == 2 && WAVES == 8 && DP == 64 && !HAS_BIAS && KT == 64 && KS == 72),
-                "LDS-direct staging: the two-tile 8-wave D = 64 kernel, padded 144-byte rows");
+  static_assert(!LD || ((WAVES == 4 || WAVES == 8) && DP == 64 && !HAS_BIAS && KT == 64 && KS == 72),
+                "LDS-direct staging: the 4- and 8-wave D = 64 kernels, padded 144-byte rows");
   // LD: one array per buffer (see bwd_dkdv_half_kernel)
   __shared__ __attribute__((aligned(16))) T Ks[LD ? 1 : 2][KT * KS];
   __shared__ __attribute__((aligned(16))) T Vs[LD ? 1 : 2][KT * KS];
@@ -626,18 +626,19 @@ void bwd_dq_half_kernel(const BwdParams p) {
   // staging registers: set S holds one 64-key stage on its way from global memory to LDS
   Chunk16 kreg[LD ? 1 : 2][LD ? 1 : NCH], vreg[LD ? 1 : 2][LD ? 1 : NCH];
   // LD: a stage tile is 64 padded rows of 9 16-byte slots (8 of data, 1 of padding), 576 slots; the
-  // lanes of wave w fill slots 64 (w + 8 j) .. + 63 (j = 0, and j = 1 for wave 0 only): slot f holds
-  // chunk f % 9 of row f / 9, and a padding slot (f % 9 == 8, never read) takes that row's chunk 0.
-  // Keys past N read as zeros: the buffer range ends at row N (the launcher checks that N rows of
-  // K and of V span less than 2^31 bytes).
-  uint32_t ldk[LD ? 2 : 1], ldv[LD ? 2 : 1];
+  // lanes of wave w fill slots 64 (w + WAVES j) .. + 63 for j < LDJ, the last j (slots 512-575) by
+  // wave 0 only: slot f holds chunk f % 9 of row f / 9, and a padding slot (f % 9 == 8, never read)
+  // takes that row's chunk 0.  Keys past N read as zeros: the buffer range ends at row N (the
+  // launcher checks that N rows of K and of V span less than 2^31 bytes).
+  constexpr int LDJ = 512 / (64 * WAVES) + 1;
+  uint32_t ldk[LD ? LDJ : 1], ldv[LD ? LDJ : 1];
   const uint32_t krb = (uint32_t)p.ks[2] * (uint32_t)sizeof(T), vrb = (uint32_t)p.vs[2] * (uint32_t)sizeof(T);
   const auto rk = make_rsrc(K, LD ? (uint32_t)p.N * krb : 0u);
   const auto rv = make_rsrc(V, LD ? (uint32_t)p.N * vrb : 0u);
   if constexpr (LD) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int f = 64 * (wave + 8 * j) + lane;
+    for (int j = 0; j < LDJ; ++j) {
+      const int f = 64 * (wave + WAVES * j) + lane;
       const int r = f / 9, ch = f % 9 == 8 ? 0 : f % 9;
       ldk[j] = (uint32_t)r * krb + (uint32_t)ch * 16u;
       ldv[j] = (uint32_t)r * vrb + (uint32_t)ch * 16u;
@@ -645,11 +646,14 @@ void bwd_dq_half_kernel(const BwdParams p) {
   }
   auto ldload = [&](int t0, T* kdst, T* vdst) {
     if constexpr (LD) {
-      buffer_load16_lds(rk, kdst + 64 * wave * 8, ldk[0] + (uint32_t)t0 * krb);
-      buffer_load16_lds(rv, vdst + 64 * wave * 8, ldv[0] + (uint32_t)t0 * vrb);
+#pragma unroll
+      for (int j = 0; j + 1 < LDJ; ++j) {
+        buffer_load16_lds(rk, kdst + 64 * (wave + WAVES * j) * 8, ldk[j] + (uint32_t)t0 * krb);
+        buffer_load16_lds(rv, vdst + 64 * (wave + WAVES * j) * 8, ldv[j] + (uint32_t)t0 * vrb);
+      }
       if (wave == 0) {
-        buffer_load16_lds(rk, kdst + 512 * 8, ldk[1] + (uint32_t)t0 * krb);
-        buffer_load16_lds(rv, vdst + 512 * 8, ldv[1] + (uint32_t)t0 * vrb);
+        buffer_load16_lds(rk, kdst + 512 * 8, ldk[LDJ - 1] + (uint32_t)t0 * krb);
+        buffer_load16_lds(rv, vdst + 512 * 8, ldv[LDJ - 1] + (uint32_t)t0 * vrb);
       }
     }
   };
@@ -760,7 +764,26 @@ static_for<0, NCH>([&](auto I) {
   };
   const auto S0 = std::integral_constant<int, 0>{};
   const auto S1 = std::integral_constant<int, 1>{};
-  if constexpr (DP <= 64 && RT == 1) {
+  if constexpr (LD) {
+    // stage it + 1 goes into the other LDS buffer while stage it computes; all loads land before
+    // the barrier that ends the stage
+    if (ntiles > 0) ldload(k_lo, Ks[0], Vs[0]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int it = 0; it < ntiles; it += 2) {
+      const int t0 = k_lo + it * KT;
+      if (it + 1 < ntiles) ldload(t0 + KT, Ks1, Vs1);
+      compute(t0, Ks[0], Vs[0]);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (it + 1 < ntiles) {
+        if (it + 2 < ntiles) ldload(t0 + 2 * KT, Ks[0], Vs[0]);
+        compute(t0 + KT, Ks1, Vs1);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+      }
+    }
+  } else if constexpr (DP <= 64 && RT == 1) {
     // global loads two stages ahead (as in dK/dV; 16K d64: 0.857 -> 0.842 ms).  At D = 128 the
     // second register set spills at two waves per SIMD, and one wave per SIMD is slower still
     // (1.64 against 1.87-2.07 ms), so that width keeps one stage of prefetch, and so does the
@@ -780,25 +803,6 @@ static_for<0, NCH>([&](auto I) {
     for (int it = 0; it < ntiles; it += 2) {
       step(it, S1, S0);
       if (it + 1 < ntiles) step(it + 1, S0, S1);
-    }
-  } else if constexpr (LD) {
-    // stage it + 1 goes into the other LDS buffer while stage it computes; all loads land before
-    // the barrier that ends the stage
-    if (ntiles > 0) ldload(k_lo, Ks[0], Vs[0]);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int it = 0; it < ntiles; it += 2) {
-      const int t0 = k_lo + it * KT;
-      if (it + 1 < ntiles) ldload(t0 + KT, Ks1, Vs1);
-      compute(t0, Ks[0], Vs[0]);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if (it + 1 < ntiles) {
-        if (it + 2 < ntiles) ldload(t0 + 2 * KT, Ks[0], Vs[0]);
-        compute(t0 + KT, Ks1, Vs1);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-      }
     }
   } else {
     gload(k_lo, S0);
@@ -865,8 +869,8 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
   constexpr int NT = 64 * WAVES, KEYS_W = 32 * KRT, BN = KEYS_W * WAVES;
   static_assert((RTS * CPR) % NT == 0, "staging must divide evenly");
   constexpr int NCH = RTS * CPR / NT;
-  static_assert(!LD || (WAVES == 8 && KRT == 1 && DP == 64 && !HAS_BIAS && Tile::SWZ && NCH == 2),
-                "LDS-direct staging: the 8-wave D = 64 kernel");
+  static_assert(!LD || ((WAVES == 4 || WAVES == 8) && KRT == 1 && DP == 64 && !HAS_BIAS && Tile::SWZ && NCH == 2),
+                "LDS-direct staging: the one-tile D = 64 kernels");
   // LD: one array per buffer, so that the compiler sees the loads into one buffer leave the other
   // one's reads alone (with one two-buffer array it waited for them before every stage's reads)
   __shared__ __attribute__((aligned(16))) T Qs[LD ? 1 : 2][RTS * KS];
@@ -940,8 +944,8 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
   // staging registers: set S holds one stage (RTS rows) on its way from global memory to LDS
   Chunk16 qreg[LD ? 1 : 2][LD ? 1 : NCH], greg[LD ? 1 : 2][LD ? 1 : NCH];
   float lreg[2] = {0.f, 0.f}, dreg[2] = {0.f, 0.f};
-  // LD: lane l of wave w fills the 16 bytes at LDS byte 16 (64 w + 512 i + l) of a stage tile for
-  // i = 0, 1: row 8 w + 64 i + l / 8 of the stage, swizzle slot l % 8, which holds chunk
+  // LD: lane l of wave w fills the 16 bytes at LDS byte 16 (64 w + 64 WAVES i + l) of a stage tile
+  // for i = 0, 1: row 8 w + 8 WAVES i + l / 8 of the stage, swizzle slot l % 8, which holds chunk
   // (l % 8) ^ lds_swz(row) of that row.  Rows past N read as zeros: the buffer range ends at row N
   // (the launcher checks that N rows of Q and of dO span less than 2^31 bytes).
   uint32_t ldq[LD ? NCH : 1], ldg[LD ? NCH : 1];
@@ -951,7 +955,7 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
   if constexpr (LD) {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
-      const int r = 8 * wave + 64 * i + (lane >> 3);
+      const int r = 8 * wave + 8 * WAVES * i + (lane >> 3);
       const uint32_t ch = (uint32_t)((lane & 7) ^ lds_swz(r));
       ldq[i] = (uint32_t)r * qrb + ch * 16u;
       ldg[i] = (uint32_t)r * grb + ch * 16u;
@@ -961,8 +965,8 @@ void bwd_dkdv_half_kernel(const BwdParams p) {
     if constexpr (LD) {
 #pragma unroll
       for (int i = 0; i < NCH; ++i) {
-        buffer_load16_lds(rq, qdst + (64 * wave + 512 * i) * 8, ldq[i] + (uint32_t)t0 * qrb);
-        buffer_load16_lds(rg, gdst + (64 * wave + 512 * i) * 8, ldg[i] + (uint32_t)t0 * grb);
+        buffer_load16_lds(rq, qdst + (64 * wave + 64 * WAVES * i) * 8, ldq[i] + (uint32_t)t0 * qrb);
+        buffer_load16_lds(rg, gdst + (64 * wave + 64 * WAVES * i) * 8, ldg[i] + (uint32_t)t0 * grb);
       }
       // rows past N: LSE2 = +inf makes their p exactly 0.  D is negated at the store, so that no
       // instruction here waits for these loads (and with them for the LDS loads issued before)
@@ -1564,6 +1568,13 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
     constexpr int R = 1;  // one 32-wide tile per wave: 2 waves per SIMD beat wider tiles at 1
     const dim3 grid((p.N + 32 * R * W - 1) / (32 * R * W), p.BH);
+    // LDS-direct staging (unbiased D = 64 kernels) where every head-dim chunk is data and the buffer
+    // ranges of N rows stay below 2^31 bytes: K/V for dq, Q/dO for dK/dV
+    const int64_t lim = int64_t(1) << 31, es = (int64_t)sizeof(T);
+    const bool ld_kv = !B && DP == 64 && p.D == 64 && (int64_t)p.N * p.ks[2] * es < lim &&
+                       (int64_t)p.N * p.vs[2] * es < lim;
+    const bool ld_qg = !B && DP == 64 && p.D == 64 && (int64_t)p.N * p.qs[2] * es < lim &&
+                       (int64_t)p.N * p.gs[2] * es < lim;
     if constexpr (!B && DP <= 64) {
       if (p.split > 1) {
         // an under-filled grid (short sequences, few heads): the key (dq) or row (dK/dV) loop cut
@@ -1574,12 +1585,20 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
         const CombineOut ck{p.part + p.part_stride, p.dk, {p.dks[0], p.dks[1], p.dks[2]}, p.scale, kkv};
         const CombineOut cv{p.part + 2 * p.part_stride, p.dv, {p.dvs[0], p.dvs[1], p.dvs[2]}, 1.f, kkv};
         if (stage < 0 || stage == 1) {
-          hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, W, false>), gs, dim3(64 * W), 0, st, p);
+          if (ld_kv) {
+            hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, W, false, DP == 64>), gs, dim3(64 * W), 0, st, p);
+          } else {
+            hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, W, false>), gs, dim3(64 * W), 0, st, p);
+          }
           if ((e = hipGetLastError()) != hipSuccess) return e;
           if (stage == 1 && (e = combine_launch<T>(p, &cq, 1, st)) != hipSuccess) return e;
         }
         if (stage < 0 || stage == 2) {
-          hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, W, false>), gs, dim3(64 * W), 0, st, p);
+          if (ld_qg) {
+            hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, W, false, DP == 64>), gs, dim3(64 * W), 0, st, p);
+          } else {
+            hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, W, false>), gs, dim3(64 * W), 0, st, p);
+          }
           if ((e = hipGetLastError()) != hipSuccess) return e;
         }
         // the whole backward sums the three gradients' partials in one launch
@@ -1617,9 +1636,7 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
           if (wide && n8 >= 256) {
             // LDS-direct staging where every head dim chunk is data (D = 64) and the buffer ranges of
             // N rows of K and V stay below 2^31 bytes
-            const bool ld = p.D == 64 && (int64_t)p.N * p.ks[2] * (int64_t)sizeof(T) < (int64_t(1) << 31) &&
-                            (int64_t)p.N * p.vs[2] * (int64_t)sizeof(T) < (int64_t(1) << 31);
-            if (ld) {
+            if (ld_kv) {
               hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, 2, 8, false, true>), grid8, dim3(512), 0, st, p);
             } else {
               hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, 2, 8, false>), grid8, dim3(512), 0, st, p);
@@ -1635,12 +1652,22 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
       if (!wide) {
         if constexpr (DP == 64) {
           if ((int64_t)grid2.x * grid2.y >= 512) {
-            hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, 8, B>), grid2, dim3(512), 0, st, p);
+            if (ld_kv) {
+              hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, 8, false, !B>), grid2, dim3(512), 0, st, p);
+            } else {
+              hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, 8, B>), grid2, dim3(512), 0, st, p);
+            }
             wide = true;
           }
         }
       }
-      if (!wide) hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, W, B>), grid, dim3(64 * W), 0, st, p);
+      if (!wide) {
+        if (ld_kv) {
+          hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, W, false, !B && DP == 64>), grid, dim3(64 * W), 0, st, p);
+        } else {
+          hipLaunchKernelGGL((bwd_dq_half_kernel<T, DP, R, W, B>), grid, dim3(64 * W), 0, st, p);
+        }
+      }
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (stage < 0 || stage == 2) {
@@ -1653,10 +1680,8 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
         if ((int64_t)g8.x * g8.y >= 512) {
           // LDS-direct staging where every head dim chunk is data (D = 64) and the buffer ranges of
           // N rows of Q and dO stay below 2^31 bytes
-          const bool ld = !B && p.D == 64 && (int64_t)p.N * p.qs[2] * (int64_t)sizeof(T) < (int64_t(1) << 31) &&
-                          (int64_t)p.N * p.gs[2] * (int64_t)sizeof(T) < (int64_t(1) << 31);
           if constexpr (!B) {
-            if (ld) {
+            if (ld_qg) {
               hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, 8, false, true>), g8, dim3(512), 0, st, p);
             } else {
               hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, 8, B>), g8, dim3(512), 0, st, p);
@@ -1667,7 +1692,13 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
           w8 = true;
         }
       }
-      if (!w8) hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, W, B>), grid, dim3(64 * W), 0, st, p);
+      if (!w8) {
+        if (ld_qg) {
+          hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, W, false, !B && DP == 64>), grid, dim3(64 * W), 0, st, p);
+        } else {
+          hipLaunchKernelGGL((bwd_dkdv_half_kernel<T, DP, R, W, B>), grid, dim3(64 * W), 0, st, p);
+        }
+      }
       e = hipGetLastError();
     }
   } else {
