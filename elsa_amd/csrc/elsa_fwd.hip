@@ -807,7 +807,12 @@ __device__ inline WgCoord causal_full_pair(int n, int BH, int P, int part_len) {
 // vector phase, and the kernel is 5% faster than the two-waves-per-SIMD fold at 16K-64K keys.
 // CF: the ping-pong launch of a causal split (causal_full_pair): every work-group's partition lies
 // wholly before its rows, so the fold needs no mask.
-template <typename T, int DP, bool PRE, bool EXACT, bool CF = false>
+// LD (D = 64): group 0 loads each stage's K and V tiles straight into LDS (buffer_load_dwordx4 ...
+// lds) at the start of its softmax phase, instead of into registers in its matrix phase and from
+// there into LDS at the end of the softmax phase.  The targets hold K_{i-1} and V_{i-2}, which the
+// other group last read in its M_{i-1} and (K, the relaxed state's rare re-formed scores) V_{i-1}
+// phases, both before this one; the barrier at the end of the phase waits for the loads.
+template <typename T, int DP, bool PRE, bool EXACT, bool CF = false, bool LD = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void phase1_pp_kernel(const Phase1Params p) {
   using M = Mfma<T>;
@@ -875,7 +880,36 @@ void phase1_pp_kernel(const Phase1Params p) {
   const uint32_t kvoff = sd0 < p.D ? (uint32_t)skey * krs + (uint32_t)sd0 * (uint32_t)sizeof(T) : kBufferOff;
   const uint32_t vvoff = sd0 < p.D ? (uint32_t)skey * vrs + (uint32_t)sd0 * (uint32_t)sizeof(T) : kBufferOff;
   const int soff = skey * KS + sd0;
-  Chunk16 kreg[NCH], vreg[NCH];
+  Chunk16 kreg[LD ? 1 : NCH], vreg[LD ? 1 : NCH];
+  // LD: a stage tile is 64 padded rows of 9 16-byte slots (8 of data, 1 of padding, never read);
+  // the lanes of group 0's wave w fill slots 64 (w + 4 j) .. + 63 (j = 0, 1, and j = 2 for wave 0
+  // only): slot f holds chunk f % 9 of key row f / 9, the padding slot that row's chunk 0
+  uint32_t ldk[LD ? 3 : 1], ldv[LD ? 3 : 1];
+  if constexpr (LD) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int f = 64 * ((wave & 3) + 4 * j) + lane;
+      const int r = f / 9, ch = f % 9 == 8 ? 0 : f % 9;
+      ldk[j] = (uint32_t)r * krs + (uint32_t)ch * 16u;
+      ldv[j] = (uint32_t)r * vrs + (uint32_t)ch * 16u;
+    }
+  }
+  // group 0: K of stage i (when i < ntiles) into kdst and V of stage iv into vdst
+  auto ldload = [&](int i, T* kdst, int iv, T* vdst) {
+    if constexpr (LD) {
+      const uint32_t kt = (uint32_t)(i * KT), vt = (uint32_t)(iv * KT);
+      const bool k_on = i < ntiles, v_on = iv >= 0;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (k_on) buffer_load16_lds(rk, kdst + 64 * (wave + 4 * j) * 8, ldk[j] + kt * krs);
+        if (v_on) buffer_load16_lds(rv, vdst + 64 * (wave + 4 * j) * 8, ldv[j] + vt * vrs);
+      }
+      if (wave == 0) {
+        if (k_on) buffer_load16_lds(rk, kdst + 512 * 8, ldk[2] + kt * krs);
+        if (v_on) buffer_load16_lds(rv, vdst + 512 * 8, ldv[2] + vt * vrs);
+      }
+    }
+  };
 
   f32x16 oacc[RT][NDT];
   // PRE: -ref in every register, the accumulator input of the stage's QK^T product
@@ -893,11 +927,16 @@ void phase1_pp_kernel(const Phase1Params p) {
   F pk[RT][NSUB][2];  // p of the last folded stage, for its P^T V in the next M phase
 
   if (grp == 0) {
-    static_for<0, NCH>([&](auto I) {
-      constexpr int ii = decltype(I)::value;
-      kreg[ii] = buffer_load16(rk, kvoff + (uint32_t)(ii * KSTEP) * krs, 0);
-      *reinterpret_cast<Chunk16*>(&Ks[0][soff + ii * KSTEP * KS]) = kreg[ii];
-    });
+    if constexpr (LD) {
+      ldload(0, Ks[0], -1, Vs[0]);
+      __builtin_amdgcn_s_waitcnt(0);  // the loads land before the barrier below
+    } else {
+      static_for<0, NCH>([&](auto I) {
+        constexpr int ii = decltype(I)::value;
+        kreg[ii] = buffer_load16(rk, kvoff + (uint32_t)(ii * KSTEP) * krs, 0);
+        *reinterpret_cast<Chunk16*>(&Ks[0][soff + ii * KSTEP * KS]) = kreg[ii];
+      });
+    }
   }
   __syncthreads();
   if (grp == 1) __syncthreads();  // group 1 sits out phase 0
@@ -928,7 +967,7 @@ void phase1_pp_kernel(const Phase1Params p) {
   for (int i = 0; i < ntiles; ++i) {
     f32x16 s[RT][NSUB];
     // ---- M_i: P^T V of stage i-1, S = K Q^T - ref of stage i
-    if (grp == 0) {  // K_{i+1}, V_i: written at the end of this group's V_i
+    if (!LD && grp == 0) {  // K_{i+1}, V_i: written at the end of this group's V_i
       const uint32_t kt = (uint32_t)(i * KT);
       static_for<0, NCH>([&](auto I) {
         constexpr int ii = decltype(I)::value;
@@ -961,6 +1000,7 @@ void phase1_pp_kernel(const Phase1Params p) {
     __builtin_amdgcn_s_setprio(0);
     __syncthreads();
     // ---- V_i: softmax of stage i
+    if (LD && grp == 0) ldload(i + 1, Ks[(i + 1) & 1], i, Vs[i & 1]);
     const int t0 = k_begin + i * KT;
     if (t0 + KT > k_end) {
 #pragma unroll
@@ -1134,13 +1174,14 @@ void phase1_pp_kernel(const Phase1Params p) {
             for (int t = 0; t < 8; ++t) pk[rt][sub][j][t] = static_cast<T>(s[rt][sub][j * 8 + t]);
       }
     }
-    if (grp == 0) {
+    if (!LD && grp == 0) {
       static_for<0, NCH>([&](auto I) {
         constexpr int ii = decltype(I)::value;
         if (i + 1 < ntiles) *reinterpret_cast<Chunk16*>(&Ks[(i + 1) & 1][soff + ii * KSTEP * KS]) = kreg[ii];
         *reinterpret_cast<Chunk16*>(&Vs[i & 1][soff + ii * KSTEP * KS]) = vreg[ii];
       });
     }
+    if constexpr (LD) __builtin_amdgcn_s_waitcnt(0);  // this phase's loads land before the barrier
     __syncthreads();
   }
   // M_n: the last stage's P^T V (group 0 at phase 2n, group 1 at 2n + 1)
@@ -1391,10 +1432,19 @@ static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
         !p.direct && !pv32 && !p.prescale_q && p.N >= kCausalSplitMin) {
       const int pairs = p.BH * causal_full_pairs(p.N, p.P, p.part_len);
       if (pairs > 0) {
+        const bool ld = p.D == 64;
         if (p.exact_max) {
-          hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, true, true>), dim3(pairs), dim3(512), 0, st, p);
+          if (ld) {
+            hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, true, true, true>), dim3(pairs), dim3(512), 0, st, p);
+          } else {
+            hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, true, true>), dim3(pairs), dim3(512), 0, st, p);
+          }
         } else {
-          hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, false, true>), dim3(pairs), dim3(512), 0, st, p);
+          if (ld) {
+            hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, false, true, true>), dim3(pairs), dim3(512), 0, st, p);
+          } else {
+            hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, false, true>), dim3(pairs), dim3(512), 0, st, p);
+          }
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -1406,21 +1456,39 @@ static hipError_t launch1h(const Phase1Params& p, hipStream_t st) {
     }
     if (!p.causal && p.part_len >= 1024 && !pv32) {
       bool done = false;
+      // D = 64: K/V staged straight into LDS (phase1_pp_kernel's LD)
+      const bool ld = p.D == 64;
       if constexpr (std::is_same<T, f16>::value) {
         if (p.prescale_q) {
           if (p.exact_max) {
-            hipLaunchKernelGGL((phase1_pp_kernel<T, DP, true, true>), g2, dim3(512), 0, st, p);
+            if (ld) {
+              hipLaunchKernelGGL((phase1_pp_kernel<T, DP, true, true, false, true>), g2, dim3(512), 0, st, p);
+            } else {
+              hipLaunchKernelGGL((phase1_pp_kernel<T, DP, true, true>), g2, dim3(512), 0, st, p);
+            }
           } else {
-            hipLaunchKernelGGL((phase1_pp_kernel<T, DP, true, false>), g2, dim3(512), 0, st, p);
+            if (ld) {
+              hipLaunchKernelGGL((phase1_pp_kernel<T, DP, true, false, false, true>), g2, dim3(512), 0, st, p);
+            } else {
+              hipLaunchKernelGGL((phase1_pp_kernel<T, DP, true, false>), g2, dim3(512), 0, st, p);
+            }
           }
           done = true;
         }
       }
       if (!done) {
         if (p.exact_max) {
-          hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, true>), g2, dim3(512), 0, st, p);
+          if (ld) {
+            hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, true, false, true>), g2, dim3(512), 0, st, p);
+          } else {
+            hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, true>), g2, dim3(512), 0, st, p);
+          }
         } else {
-          hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, false>), g2, dim3(512), 0, st, p);
+          if (ld) {
+            hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, false, false, true>), g2, dim3(512), 0, st, p);
+          } else {
+            hipLaunchKernelGGL((phase1_pp_kernel<T, DP, false, false>), g2, dim3(512), 0, st, p);
+          }
         }
       }
       return hipGetLastError();
