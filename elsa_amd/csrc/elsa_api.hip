@@ -65,9 +65,10 @@ size_t fwd_workspace_bytes(int64_t parts, int64_t bh, int64_t q_chunk, int64_t d
   return 2 * align256(rows * 4) + align256(rows * d * dtype_size(sdt));
 }
 
-// Partition routing for 256 CUs: at least ~2048 Phase-1 workgroups when the
-// query side alone does not provide them, partitions of >= 512 keys, and at
-// least two partitions from 8K keys on so long sequences keep the two-pass merge.
+// Partition routing for 256 CUs: about 1024 Phase-1 workgroups when the query side alone
+// does not provide them, partitions of >= 512 keys (>= 1024 and one round of the chip where
+// the ping-pong fold runs), and at least two partitions from 8K keys on so long sequences
+// keep the two-pass merge.
 int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
   if (!a || !pl) return fail(ELSA_ERR_INVALID, "null argument");
   int rc = check_common(a->batch, a->heads, a->seq_len, a->head_dim, a->dtype, a->q, a->k, a->v);
@@ -92,8 +93,8 @@ int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
     const int64_t q_tiles = bh * cdiv(q_rows, bm);
     // about 1024 Phase-1 workgroups (4 per CU): at B1 H8 d64 fp16 16K, Phase 1 + Phase 2 took
     // 0.594 ms with 2 partitions against 0.605 ms with 4 (2048 workgroups); 64K 9.06 / 9.17 /
-    // 9.35 ms with 4 / 8 / 16; the forward at 1K and at ViT's 1025 and 4097 tokens (B8 H3)
-    // stays within 3% from 1 to 8 partitions
+    // 9.35 ms with 4 / 8 / 16; the forward at 1K and at ViT's 1025 tokens (B8 H3) stays within
+    // 3% from 1 to 8 partitions
     int64_t p = cdiv(1024, q_tiles);
     p = std::min<int64_t>(p, std::max<int64_t>(1, n / 512));
     if (n >= 8192) p = std::max<int64_t>(p, 2);
@@ -104,10 +105,33 @@ int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
     // 1.344 / 1.227 / 1.199 ms.
     if (a->is_causal && n >= 8192) p = cdiv(n, std::min<int64_t>(8192, std::max<int64_t>(2048, n / 4)));
     p = std::max<int64_t>(p, 1);
+    // the ping-pong fold (fp16/bf16 at d = 64 without bias or causal mask, 16-bit summaries; the
+    // launcher's condition) runs 512-row work-groups over partitions of at least 1024 keys: B1 H8 4K
+    // forward 0.060 -> 0.052 ms (fp16) and 0.060 -> 0.054 ms (bf16) with four of them against eight
+    // of 512 (2K keeps four of 512: 0.025 against 0.040 ms with two).  Its partition count minimises
+    // rounds x (partition keys + 768): ceil(work-groups / 256 CUs) rounds, each as long as a
+    // partition plus a work-group's fixed cost (Q load, summary stores, the two fill phases),
+    // which the measurements put near 768 keys; ties keep fewer partitions.  Forward ms (Phase 1 +
+    // Phase 2, fp16 d64) against the 1024-workgroup target of 256-row blocks: B1 H8 8K 0.155 ->
+    // 0.134 (4 -> 2 partitions), B2 H8 4K 0.097 -> 0.079 (4 -> 2), B4 H8 4K 0.158 -> 0.133 (2 -> 1),
+    // B8 H3 N4097 0.155 -> 0.128 (3 -> 1), B1 H4 16K 0.269 -> 0.256 (4 -> 2), B1 H8 N6000 0.129 ->
+    // 0.092 (6 -> 2), B1 H8 N12000 0.352 -> 0.323 (3 -> 2); the north star keeps 2.
+    const bool pp = !a->is_causal && !a->bias.ptr && a->dtype != ELSA_F32 && dp == 64 && bm == 256 &&
+                    !(a->dtype == ELSA_F16 && a->summary_dtype == ELSA_F32);
+    if (pp && n >= 4096) {
+      const int64_t tiles = bh * cdiv(q_rows, 512);
+      const int64_t p_lo = n >= 8192 ? 2 : 1, p_hi = std::max<int64_t>(p_lo, n / 1024);
+      int64_t best_cost = -1;
+      for (int64_t c = p_lo; c <= p_hi; ++c) {
+        const int64_t len = cdiv(cdiv(n, c), kt) * kt;
+        const int64_t cost = cdiv(tiles * cdiv(n, len), 256) * (len + 768);
+        if (best_cost < 0 || cost < best_cost) {
+          best_cost = cost;
+          p = c;
+        }
+      }
+    }
     part = cdiv(cdiv(n, p), kt) * kt;
-    // the ping-pong fold (fp16/bf16 at d = 64 without bias or causal mask) takes partitions of at
-    // least 1024 keys: B1 H8 4K forward 0.060 -> 0.052 ms (fp16) and 0.060 -> 0.054 ms (bf16) with
-    // four of them against eight of 512 (2K keeps four of 512: 0.025 against 0.040 ms with two)
     if (!a->is_causal && !a->bias.ptr && a->dtype != ELSA_F32 && dp == 64 && n >= 4096 && part < 1024) part = 1024;
     if (a->is_causal && p > 1) {  // one partition stays whole: its launch applies the finalize
       // causal partitions hold whole row blocks, which Phase 1's longest-first order needs;

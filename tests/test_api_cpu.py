@@ -85,6 +85,54 @@ def test_plan_ping_pong_partitions_from_4k(n, dtype, d, causal, parts, part):
     assert rc == 0 and (p.partitions, p.partition_len) == (parts, part)
 
 
+def _pp_rounds_model(n, bh, q_rows=None):
+    """The partition count of the ping-pong routing, restated: the count in [1 or 2, n / 1024] that
+    minimises ceil(work-groups / 256) x (partition keys + 768), ties to the fewer."""
+    tiles = bh * -(-(q_rows or n) // 512)
+    lo = 2 if n >= 8192 else 1
+    best = None
+    for c in range(lo, max(lo, n // 1024) + 1):
+        part = -(-(-(-n // c)) // 64) * 64
+        cost = -(-(tiles * -(-n // part)) // 256) * (part + 768)
+        if best is None or cost < best[0]:
+            best = (cost, part)
+    return best[1]
+
+
+# the ping-pong fold's routing: one round of 512-row work-groups where the grid allows (measured
+# bests: B1 H8 8K 2 partitions, B4 H8 4K and B8 H3 N4097 one, B2 H8 N4097 three, B1 H8 N12000 four)
+@pytest.mark.parametrize("n,bh,dtype,parts,part", [
+    (16384, (1, 8), _lib.ELSA_F16, 2, 8192),   # the north star keeps two
+    (8192, (1, 8), _lib.ELSA_F16, 2, 4096),
+    (8192, (1, 8), _lib.ELSA_BF16, 2, 4096),
+    (4096, (4, 8), _lib.ELSA_F16, 1, 4096),    # one partition (n < 8K): the finalize is fused
+    (4097, (8, 3), _lib.ELSA_F16, 1, 4097),
+    (4097, (2, 8), _lib.ELSA_F16, 3, 1408),
+    (12000, (1, 8), _lib.ELSA_F16, 4, 3008),
+    (65536, (1, 8), _lib.ELSA_F16, 2, 32768),
+    (16384, (1, 2), _lib.ELSA_F16, 4, 4096),
+])
+def test_plan_ping_pong_one_round(n, bh, dtype, parts, part):
+    rc, p = _plan(_args(n=n, bh=bh, dtype=dtype))
+    assert rc == 0 and (p.partitions, p.partition_len) == (parts, part)
+    assert min(part, n) == min(_pp_rounds_model(n, bh[0] * bh[1]), n)
+
+
+def test_plan_ping_pong_rule_only_where_the_ping_pong_fold_runs():
+    # fp16 inputs with fp32 summaries run the 4-wave fold (p unrounded for P.V): ~1024 256-row work-groups
+    a = _args(n=8192)
+    a.summary_dtype = _lib.ELSA_F32
+    rc, p = _plan(a)
+    assert rc == 0 and (p.partitions, p.partition_len) == (4, 2048)
+    # fp32 and d128 (128-row blocks, 512 of them at B1 H8 8K): two partitions of the 1024 target
+    rc, p = _plan(_args(n=8192, dtype=_lib.ELSA_F32))
+    assert rc == 0 and (p.block_m, p.partitions) == (128, 2)
+    rc, p = _plan(_args(n=8192, d=128))
+    assert rc == 0 and (p.block_m, p.partitions) == (128, 2)
+    rc, p = _plan(_args(n=8192, bh=(1, 2), d=32))  # the 4-wave fold at d32: 1024 / 64 = 16 of 512 keys
+    assert rc == 0 and (p.partitions, p.partition_len) == (16, 512)
+
+
 @pytest.mark.parametrize("n,bh,d", [(49, (8, 3), 32), (197, (8, 3), 64), (1024, (1, 8), 64), (65536, (1, 8), 64),
                                     (4097, (8, 3), 64), (300, (1, 2), 128)])
 def test_plan_partitions_cover_sequence(n, bh, d):

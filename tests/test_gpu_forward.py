@@ -37,6 +37,8 @@ CASES = [
     ((1, 2, 1025, 64), "fp16", False, 256, None),
     ((1, 2, 4097, 64), "fp16", True, None, None),
     ((1, 2, 4097, 64), "fp16", False, 1024, None),
+    ((1, 2, 4096, 64), "fp16", False, 4096, None),  # the ping-pong fold over one partition, finalize fused
+    ((1, 2, 4097, 64), "bf16", False, 4097, None),
     ((1, 2, 2048, 64), "fp16", True, None, None),
     ((1, 3, 777, 64), "fp16", True, 256, 256),   # causal q-chunks: the row-block order without longest first
     ((1, 2, 1000, 64), "bf16", True, 200, None),  # causal partitions not a multiple of the row block

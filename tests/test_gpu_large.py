@@ -259,6 +259,8 @@ TRAIN = [
     ((1, 4, 4096, 64), "fp16", "spikes", 1024),
     ((2, 8, 4097, 64), "fp16", None, 2048),    # ragged: a last partition of one key, its stage masked
     ((2, 16, 2048, 64), "bf16", None, 1024),
+    ((4, 8, 4096, 64), "fp16", None, None),    # one round of 512-row work-groups: one partition, finalize fused
+    ((8, 3, 4097, 64), "bf16", None, None),    # ViT-T 1024 px: one partition, a ragged last stage
 ]
 
 
