@@ -277,6 +277,42 @@ def test_strided_backward_is_bitwise_the_dense_one(dt, n, causal, d, bh):
         assert torch.equal(a, ref)
 
 
+@pytest.mark.parametrize("dt,n,h,causal", [("fp16", 16384, 8, False), ("bf16", 16384, 8, True), ("fp16", 1100, 1, False)])
+def test_backward_over_row_ranges_past_2gib_is_bitwise_the_dense_one(dt, n, h, causal):
+    """q, k and v as views of [N, S] buffers (heads 64 elements apart within a row) whose N rows span
+    2^31 bytes or more: the LDS-direct loads address a 32-bit buffer range, so the backward stages
+    K/V and Q/dO through registers there (the 8-wave two-tile dq, the 8-wave one-tile dq and dK/dV
+    at 16K, the split 4-wave kernels at N1100).  Both stagings move the same tiles into the same
+    LDS layout: the same bits as the backward on dense copies, which runs the LDS-direct kernels."""
+    from elsa_amd.attention import _BiasMeta
+    from elsa_amd.attention_bwd import _backward, _with_state
+
+    d = 64
+    need = -(-(1 << 31) // (2 * n))
+    row = max(65536, (need + 63) // 64 * 64)  # n * row * 2 bytes >= 2^31
+    assert n * row * 2 >= 1 << 31
+    describe(f"backward over {n} rows of stride {row} elements ({n * row * 2 / 2**30:.2f} GiB), {dt} h={h} causal={causal}")
+    g = torch.Generator(device="cuda").manual_seed(n + h)
+    views = []
+    for _ in range(3):
+        buf = torch.empty((n, row), dtype=TORCH_DT[dt], device="cuda")
+        v = buf.as_strided((1, h, n, d), (n * row, d, row, 1))
+        v.copy_(torch.randn((1, h, n, d), generator=g, device="cuda"))
+        views.append(v)
+    q, k, v = views
+    do = torch.randn((1, h, n, d), generator=g, device="cuda").to(TORCH_DT[dt])
+    out, rm, rz = _with_state(q, k, v, is_causal=causal)
+    meta = _BiasMeta(None, 0, 0, 0, 0, False)
+    strided = _backward(q, k, v, out, do, meta, is_causal=causal, row_m=rm, row_z=rz)
+    dense = _backward(q.contiguous(), k.contiguous(), v.contiguous(), out, do, meta, is_causal=causal, row_m=rm,
+                      row_z=rz)
+    torch.cuda.synchronize()
+    for name, a, ref in zip("qkv", strided, dense):
+        assert torch.isfinite(ref).all()
+        assert torch.equal(a, ref), f"d{name} differs from the dense backward"
+    del views, q, k, v
+
+
 def test_strided_backward_with_head_broadcast_inputs():
     """k and v broadcast over heads (zero head stride) are read in place; the gradients
     per head match those of the materialised copies."""
