@@ -367,6 +367,14 @@ def main() -> int:
     print(f"bench: {shape} {args.dtype} causal={causal} steps={args.steps} warmup={args.warmup}", file=sys.stderr,
           flush=True)
 
+    # ---- per-kernel HIP-event timing through the C ABI, on the stream the kernels run on (first, so
+    # that the GPU clock has left its idle state before the warm-up and timed steps below)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    kern_ms, plan, out = _kernel_ms(lib, stream, q, k, v, do, causal, args.block_n, args.steps)
+    print("bench: kernels " + ", ".join(f"{k_}={v_:.3f}ms" for k_, v_ in kern_ms.items()), file=sys.stderr,
+          flush=True)
+
     # one training step through the reference's training entry point (its benchmarks/bench_bwd.py
     # times twopass_attention_train(...).backward(dout)): forward with the row state the backward
     # reads, then the recompute backward; torch.autograd.grad returns the gradients without
@@ -390,13 +398,6 @@ def main() -> int:
     wall = time.perf_counter() - t0
     ms_step = ev0.elapsed_time(ev1) / args.steps
     print(f"bench: step {ms_step:.3f} ms (wall {wall * 1e3 / args.steps:.3f} ms)", file=sys.stderr, flush=True)
-
-    # ---- per-kernel HIP-event timing through the C ABI, on the stream the kernels run on
-    lib = _lib.load()
-    stream = torch.cuda.current_stream(dev)
-    kern_ms, plan, out = _kernel_ms(lib, stream, q, k, v, do, causal, args.block_n, args.steps)
-    print("bench: kernels " + ", ".join(f"{k_}={v_:.3f}ms" for k_, v_ in kern_ms.items()), file=sys.stderr,
-          flush=True)
 
     # ---- the matrix cores' sustained rate on operands with this run's value statistics
     ceiling = _mfma_ceiling(args, lib, dev, stream)
