@@ -80,12 +80,6 @@ __device__ __host__ constexpr inline int key_of_reg(int r, int g) { return 16 * 
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-template <typename T>
-__device__ inline float to_f32(T x) { return static_cast<float>(x); }
-
-template <typename T>
-__device__ inline T from_f32(float x) { return static_cast<T>(x); }
-
 // Load KP elements (one MFMA operand fragment) from memory; `ok` false gives zeros.
 template <typename T>
 __device__ inline typename Mfma<T>::frag load_frag(const T* p, bool ok) {
