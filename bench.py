@@ -181,8 +181,9 @@ def _kernel_ms(lib, stream, q, k, v, do, causal, block_n, steps):
     Phase 1 + Phase 2 run the training forward (the relaxed row state the backward reads); the
     three backward stages run on that forward's output and row state.  A plan of one partition
     is timed as ``elsa_fwd`` runs it, one Phase-1 launch with the finalize fused into its epilogue
-    (phase2_merge is then 0: no launch).  Returns (ms by kernel, the forward plan, the forward
-    output)."""
+    (phase2_merge is then 0: no launch); where the dq kernel runs the preprocess (fp16/bf16 at
+    d = 64) bwd_preprocess is 0 the same way.  Returns (ms by kernel, the forward plan, the
+    forward output)."""
     import torch
 
     from elsa_amd import _lib
@@ -209,12 +210,15 @@ def _kernel_ms(lib, stream, q, k, v, do, causal, block_n, steps):
     chunks = [(s_, min(qc, N - s_)) for s_ in range(0, N, qc)]
 
     fused = plan["partitions"] == 1
+    # fp16/bf16 at d = 64 (dense operands, N rows under 2 GiB): the dq kernels run the preprocess of
+    # their rows, and a whole backward (elsa_bwd) launches no preprocess kernel
+    pre_fused = q.dtype in (torch.float16, torch.bfloat16) and D == 64 and N * D * q.element_size() < 2**31
     launches = {
         "phase1_fold": ((lambda: [lib.elsa_fwd(ctypes.byref(fa), sh)]) if fused else
                         (lambda: [lib.elsa_phase1(ctypes.byref(fa), s_, n_, sh) for s_, n_ in chunks])),
         "phase2_merge": None if fused else (lambda: [lib.elsa_phase2(ctypes.byref(fa), s_, n_, sh)
                                                      for s_, n_ in chunks]),
-        "bwd_preprocess": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 0, sh)],
+        "bwd_preprocess": None if pre_fused else (lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 0, sh)]),
         "bwd_dq": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 1, sh)],
         "bwd_dkdv": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 2, sh)],
     }
@@ -427,8 +431,8 @@ def main() -> int:
     kernels = {}
     for name, ms in kern_ms.items():
         bound, work = algo[name]
-        if ms == 0.0:  # Phase 2 fused into the Phase-1 launch (one partition)
-            kernels[name] = {"ms": 0.0, "fused_into": "phase1_fold"}
+        if ms == 0.0:  # Phase 2 fused into the Phase-1 launch (one partition), the preprocess into dq
+            kernels[name] = {"ms": 0.0, "fused_into": "bwd_dq" if name == "bwd_preprocess" else "phase1_fold"}
         elif bound == "mfma":
             ach = work / (ms * 1e-3) / 1e12
             kernels[name] = {"ms": round(ms, 4), "tflops": round(ach, 1), "frac_peak": round(ach / peak, 4)}

@@ -131,6 +131,22 @@ __device__ inline void f32_stage_store2(const Chunk16 (&reg)[NR], float* tr, flo
 }
 
 // ------------------------------------------------------------------ preprocess
+// LSE2 = m + log2(max(z, 1e-30)) (attention_bwd.py:224), formed in double and split into its fp32
+// rounding hi and the remainder lo, so that the fp32 kernels' p = exp2(s*c - LSE2) does not carry
+// the half-ulp of a ~15-magnitude LSE2 (3e-7 relative, the same for a whole row) into every
+// gradient of that row.  A row with no valid key (z == 0) gets +inf instead of -inf, so that p is 0
+// without a test.
+__device__ inline void lse2_split(float m, float z, float& hi, float& lo) {
+  if (z > 0.f) {
+    const double l = (double)m + log2((double)fmaxf(z, 1.0e-30f));
+    hi = (float)l;
+    lo = (float)(l - (double)hi);
+  } else {
+    hi = __builtin_huge_valf();
+    lo = 0.f;
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdParams p) {
   // grid: x = block of 32 rows, y = batch * head.  The 8 lanes of a row read its 16-byte
@@ -159,21 +175,10 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const BwdParams p) {
   if (!ok || sub != 0) return;
   const int64_t i = (int64_t)bh * p.N + row;
   p.d_row[i] = acc;
-  // LSE2 = m + log2(max(z, 1e-30)) (attention_bwd.py:224), formed in double and split into
-  // its fp32 rounding and the remainder, so that the fp32 kernels' p = exp2(s*c - LSE2) does
-  // not carry the half-ulp of a ~15-magnitude LSE2 (3e-7 relative, the same for a whole row)
-  // into every gradient of that row.  A row with no valid key (z == 0) stores +inf instead
-  // of -inf so that p is 0 without a test.
-  const float z = p.row_z[i];
-  if (z > 0.f) {
-    const double l = (double)p.row_m[i] + log2((double)fmaxf(z, 1.0e-30f));
-    const float hi = (float)l;
-    p.lse_row[i] = hi;
-    p.lse_lo[i] = (float)(l - (double)hi);
-  } else {
-    p.lse_row[i] = __builtin_huge_valf();
-    p.lse_lo[i] = 0.f;
-  }
+  float lhi, llo;
+  lse2_split(p.row_m[i], p.row_z[i], lhi, llo);
+  p.lse_row[i] = lhi;
+  p.lse_lo[i] = llo;
 }
 
 // ------------------------------------------------------------------ dq
@@ -550,9 +555,17 @@ void bwd_dq_half_kernel(const BwdParams p) {
   const int tr_row = 8 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
+  // split (the 4-wave one-tile kernel only, below): grid z cuts the key loop into ranges
+  constexpr bool CAN_SPLIT = RT == 1 && WAVES == 4 && (DP == 128 || (!HAS_BIAS && DP <= 64));
   F qf[RT][NKK], gf[RT][NKK];
   float lse[RT], dd[RT];
   bool live[RT];
+  // LD (unbiased, D = 64): the preprocess of these rows runs here, in bwd_pre_kernel's order (per
+  // 16-byte chunk of a row an fma chain over its 8 elements from zero, then the chunk sums pairwise,
+  // ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)); lanes c and c + 32 hold the even and odd
+  // chunks of row c), so a whole backward needs no preprocess launch; the work-groups of the first
+  // key range store D and LSE2 for the dK/dV kernel
+  const T* O = static_cast<const T*>(p.out) + bi * p.os[0] + hi * p.os[1];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int row = row0 + rt * 32 + c;
@@ -564,8 +577,31 @@ void bwd_dq_half_kernel(const BwdParams p) {
       qf[rt][kk] = load_frag<T>(Q + (int64_t)rs * p.qs[2] + d0, ok && d0 < p.D);
       gf[rt][kk] = load_frag<T>(dO + (int64_t)rs * p.gs[2] + d0, ok && d0 < p.D);
     }
-    lse[rt] = ok ? p.lse_row[(int64_t)bh * p.N + row] : __builtin_huge_valf();
-    dd[rt] = ok ? p.d_row[(int64_t)bh * p.N + row] : 0.f;
+    const int64_t ri = (int64_t)bh * p.N + rs;
+    if constexpr (LD) {
+      float pair[NKK];
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk) {
+        const F of = load_frag<T>(O + (int64_t)rs * p.os[2] + kk * 16 + g * 8, ok);
+        float a = 0.f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) a = fmaf(static_cast<float>(of[t]), static_cast<float>(gf[rt][kk][t]), a);
+        pair[kk] = a + __shfl_xor(a, 32);
+      }
+      const float dsum = (pair[0] + pair[1]) + (pair[2] + pair[3]);
+      float lhi, llo;
+      lse2_split(p.row_m[ri], p.row_z[ri], lhi, llo);
+      if (ok && g == 0 && (!CAN_SPLIT || wg.z == 0)) {
+        p.d_row[ri] = dsum;
+        p.lse_row[ri] = lhi;
+        p.lse_lo[ri] = llo;
+      }
+      lse[rt] = ok ? lhi : __builtin_huge_valf();
+      dd[rt] = ok ? dsum : 0.f;
+    } else {
+      lse[rt] = ok ? p.lse_row[ri] : __builtin_huge_valf();
+      dd[rt] = ok ? p.d_row[ri] : 0.f;
+    }
     live[rt] = ok && lse[rt] < __builtin_huge_valf();
   }
   const int k_end = p.causal ? wg_last + 1 : p.N;
@@ -573,7 +609,6 @@ void bwd_dq_half_kernel(const BwdParams p) {
   // stages (one range when unsplit).  D = 128 never splits (bwd_splits) but keeps these run-time
   // bounds: with constant ones its register allocation spilled (20 bytes per lane, 468 biased;
   // 16K dq 1.698 -> 1.653 ms without)
-  constexpr bool CAN_SPLIT = RT == 1 && WAVES == 4 && (DP == 128 || (!HAS_BIAS && DP <= 64));
   const int k_lo = CAN_SPLIT ? min(k_end, wg.z * p.split_len) : 0;
   const int k_hi = CAN_SPLIT ? min(k_end, k_lo + p.split_len) : k_end;
   // a causal key range past this row block's last row adds nothing: no partial is written, and
@@ -1559,7 +1594,15 @@ template <typename T, int DP, bool B>
 static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
   constexpr int W = 4;
   hipError_t e = hipSuccess;
-  if (stage < 0 || stage == 0) {
+  // LDS-direct staging (unbiased fp16/bf16 D = 64 kernels) where the buffer ranges of N rows stay
+  // below 2^31 bytes: K/V for dq, Q/dO for dK/dV.  The LDS-direct dq kernels also run the
+  // preprocess of their rows, so a whole backward then launches no bwd_pre_kernel.
+  const int64_t lim = int64_t(1) << 31, es = (int64_t)sizeof(T);
+  const bool ld_kv = sizeof(T) == 2 && !B && DP == 64 && p.D == 64 && (int64_t)p.N * p.ks[2] * es < lim &&
+                     (int64_t)p.N * p.vs[2] * es < lim;
+  const bool ld_qg = sizeof(T) == 2 && !B && DP == 64 && p.D == 64 && (int64_t)p.N * p.qs[2] * es < lim &&
+                     (int64_t)p.N * p.gs[2] * es < lim;
+  if (stage == 0 || (stage < 0 && !ld_kv)) {
     if ((e = pre_launch<T>(p, st)) != hipSuccess) return e;
   }
   if constexpr (DP == 32) {
@@ -1568,13 +1611,6 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
     constexpr int R = 1;  // one 32-wide tile per wave: 2 waves per SIMD beat wider tiles at 1
     const dim3 grid((p.N + 32 * R * W - 1) / (32 * R * W), p.BH);
-    // LDS-direct staging (unbiased D = 64 kernels) where every head-dim chunk is data and the buffer
-    // ranges of N rows stay below 2^31 bytes: K/V for dq, Q/dO for dK/dV
-    const int64_t lim = int64_t(1) << 31, es = (int64_t)sizeof(T);
-    const bool ld_kv = !B && DP == 64 && p.D == 64 && (int64_t)p.N * p.ks[2] * es < lim &&
-                       (int64_t)p.N * p.vs[2] * es < lim;
-    const bool ld_qg = !B && DP == 64 && p.D == 64 && (int64_t)p.N * p.qs[2] * es < lim &&
-                       (int64_t)p.N * p.gs[2] * es < lim;
     if constexpr (!B && DP <= 64) {
       if (p.split > 1) {
         // an under-filled grid (short sequences, few heads): the key (dq) or row (dK/dV) loop cut

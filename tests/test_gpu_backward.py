@@ -496,9 +496,12 @@ def test_bwd_dbias_matches_bwd_then_dbias(dt, shape, bias_shape, causal):
 
 
 # elsa_bwd_stage 0 / 1 / 2 launched one by one (what bench.py times) against elsa_bwd in one call,
-# which sums the split backward's dq, dK and dV partials in a single combine launch: the same bits.
+# which sums the split backward's dq, dK and dV partials in a single combine launch and, at d = 64,
+# runs the preprocess inside the dq kernels: the same bits.
 @pytest.mark.parametrize("shape,dt,causal", [((1, 8, 1024, 64), "fp16", False), ((8, 3, 1025, 64), "bf16", False),
-                                             ((1, 4, 2048, 64), "fp16", True), ((2, 32, 1024, 64), "fp16", False)])
+                                             ((1, 4, 2048, 64), "fp16", True), ((2, 32, 1024, 64), "fp16", False),
+                                             ((1, 8, 16384, 64), "fp16", False), ((1, 8, 8192, 64), "bf16", True),
+                                             ((1, 4, 1000, 32), "fp16", False)])
 def test_backward_stages_one_by_one_are_the_whole_backward(shape, dt, causal):
     import ctypes
     import math
@@ -529,10 +532,12 @@ def test_backward_stages_one_by_one_are_the_whole_backward(shape, dt, causal):
 
 # The split backward's causal work-groups whose range holds nothing write no partials, and the
 # combine skips those ranges and any range that starts past N.  With the workspace filled with NaN
-# first, a partial read that no work-group wrote shows up in the gradients.
+# first, a partial read that no work-group wrote shows up in the gradients, and so does a row's D or
+# LSE2 that the dq kernels (the preprocess at d = 64) left unwritten for the dK/dV kernel.
 @pytest.mark.parametrize("shape,causal", [((1, 4, 2049, 64), True), ((1, 4, 2049, 64), False),
                                           ((1, 8, 2048, 64), True), ((8, 3, 1025, 64), True),
-                                          ((1, 2, 4097, 64), True)])
+                                          ((1, 2, 4097, 64), True), ((1, 8, 16385, 64), False),
+                                          ((1, 8, 8192, 64), True)])
 def test_split_backward_reads_only_written_partials(shape, causal):
     import ctypes
     import math
