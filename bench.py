@@ -213,37 +213,58 @@ def _kernel_ms(lib, stream, q, k, v, do, causal, block_n, steps):
     # fp16/bf16 at d = 64 (dense operands, N rows under 2 GiB): the dq kernels run the preprocess of
     # their rows, and a whole backward (elsa_bwd) launches no preprocess kernel
     pre_fused = q.dtype in (torch.float16, torch.bfloat16) and D == 64 and N * D * q.element_size() < 2**31
+    # each launch set takes the stream handle it launches on
     launches = {
-        "phase1_fold": ((lambda: [lib.elsa_fwd(ctypes.byref(fa), sh)]) if fused else
-                        (lambda: [lib.elsa_phase1(ctypes.byref(fa), s_, n_, sh) for s_, n_ in chunks])),
-        "phase2_merge": None if fused else (lambda: [lib.elsa_phase2(ctypes.byref(fa), s_, n_, sh)
-                                                     for s_, n_ in chunks]),
-        "bwd_preprocess": None if pre_fused else (lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 0, sh)]),
-        "bwd_dq": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 1, sh)],
-        "bwd_dkdv": lambda: [lib.elsa_bwd_stage(ctypes.byref(ba), 2, sh)],
+        "phase1_fold": ((lambda h: [lib.elsa_fwd(ctypes.byref(fa), h)]) if fused else
+                        (lambda h: [lib.elsa_phase1(ctypes.byref(fa), s_, n_, h) for s_, n_ in chunks])),
+        "phase2_merge": None if fused else (lambda h: [lib.elsa_phase2(ctypes.byref(fa), s_, n_, h)
+                                                       for s_, n_ in chunks]),
+        "bwd_preprocess": None if pre_fused else (lambda h: [lib.elsa_bwd_stage(ctypes.byref(ba), 0, h)]),
+        "bwd_dq": lambda h: [lib.elsa_bwd_stage(ctypes.byref(ba), 1, h)],
+        "bwd_dkdv": lambda h: [lib.elsa_bwd_stage(ctypes.byref(ba), 2, h)],
     }
     kern_ms = {}
     for name, fn in launches.items():
         if fn is None:
             kern_ms[name] = 0.0
             continue
-        for rc in fn():
+        for rc in fn(sh):
             _lib.check(rc, name)
         torch.cuda.synchronize()
         # warm-up of about 25 ms of GPU work: after a host-side phase (drawing the next case's inputs)
         # the GPU clock ramps up over several ms, and a single 1 ms launch set would be timed at the
         # idle clock (causal 32K Phase 1 measured 1.31 ms after an idle gap, 1.13 ms when warm)
         t0 = time.perf_counter()
-        fn()
+        fn(sh)
         torch.cuda.synchronize()
         one = max(time.perf_counter() - t0, 1e-6)
         for _ in range(min(200, int(0.025 / one))):
-            fn()
+            fn(sh)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        if one < 2e-4:
+            # a launch set shorter than about 0.2 ms: an eager loop of ctypes launches would time the
+            # host's launch rate, so REPS of them are captured in a graph and its replays are timed
+            reps = 20
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                hc = torch.cuda.current_stream().cuda_stream
+                for _ in range(reps):
+                    for rc in fn(hc):
+                        _lib.check(rc, name)
+            graph.replay()
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(steps):
+                graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            kern_ms[name] = e0.elapsed_time(e1) / (steps * reps)
+            del graph
+            continue
         e0.record(stream)
         for _ in range(steps):
-            fn()
+            fn(sh)
         e1.record(stream)
         torch.cuda.synchronize()
         kern_ms[name] = e0.elapsed_time(e1) / steps
