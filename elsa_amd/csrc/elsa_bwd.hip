@@ -234,14 +234,19 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt) acc[dt] = f32x16{};
   const int k_end = p.causal ? wg_last + 1 : p.N;
+  // split (bwd_splits; 1 range of N keys otherwise): this work-group's keys [k_lo, k_hi) over grid z,
+  // whole 64-key ranges, so a stage never straddles a range end short of k_end.  An empty range
+  // writes no partial, and the combine (kind 0 past N, kind 1 past a causal row block) skips it.
+  const int k_lo = min(k_end, (int)wg.z * p.split_len), k_hi = min(k_end, k_lo + p.split_len);
+  if (p.split > 1 && k_lo >= k_hi) return;
   constexpr int CPR = DP / 4;  // 16-byte chunks per key row
 
-  for (int t0 = 0; t0 < k_end; t0 += TT) {
+  for (int t0 = k_lo; t0 < k_hi; t0 += TT) {
     __syncthreads();
-    for (int ci = tid; ci < TT * CPR; ci += NT) {  // keys >= k_end and d >= D are zeros
+    for (int ci = tid; ci < TT * CPR; ci += NT) {  // keys >= k_hi and d >= D are zeros
       const int r = ci / CPR, d0 = (ci % CPR) * 4, key = t0 + r;
       f32x4 kv{}, vv{};
-      if (key < k_end && d0 < p.D) {
+      if (key < k_hi && d0 < p.D) {
         kv = *reinterpret_cast<const f32x4*>(K + (int64_t)key * p.ks[2] + d0);
         vv = *reinterpret_cast<const f32x4*>(V + (int64_t)key * p.vs[2] + d0);
       }
@@ -267,12 +272,12 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
         }
       }
     }
-    const bool full = !HAS_BIAS && (t0 + TT <= k_end) && (!p.causal || t0 + TT - 1 <= wg_row0 + wave * 32);
+    const bool full = !HAS_BIAS && (t0 + TT <= k_hi) && (!p.causal || t0 + TT - 1 <= wg_row0 + wave * 32);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = t0 + key_of_reg(r, g);
       bool ok = live;
-      if (!full) ok = ok && key < k_end && (!p.causal || key <= my_row);
+      if (!full) ok = ok && key < k_hi && (!p.causal || key <= my_row);
       // s*c - LSE2 with one rounding of the (small) difference, then LSE2's low part
       float x = fmaf(s[r], p.scale_log2, -lse) - lse_lo;
       if constexpr (HAS_BIAS) x = ok ? fmaf(load_bias_b(p.bias, bi, hi, my_row, key), kLog2e, x) : x;
@@ -299,6 +304,14 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
     for (int dt = 0; dt < C::NDT; ++dt) acc[dt] += st[dt];
   }
   if (!row_ok) return;
+  if (p.split > 1) {  // this key range's unscaled dQ: the combine sums the ranges and scales
+    float* dst = p.part + (((int64_t)wg.z * p.BH + bh) * p.N + my_row) * p.dp;
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dst[dt * 32 + drow(r, g)] = acc[dt][r];
+    return;
+  }
   T* out = static_cast<T*>(p.dq) + bi * p.dqs[0] + hi * p.dqs[1] + (int64_t)my_row * p.dqs[2];
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt)
@@ -369,7 +382,12 @@ void bwd_dkdv_kernel(const BwdParams p) {
     dv[dt] = f32x16{};
   }
   const int r_begin = p.causal ? (wg_key0 / TT) * TT : 0;
-  const int ntiles = (p.N - r_begin + TT - 1) / TT;
+  // split (bwd_splits; 1 range of N rows otherwise): this work-group's rows [r_lo, r_hi) over grid z,
+  // whole 64-row ranges.  An empty range writes no partial, and the combine (kind 0 past N, kind 2
+  // before a causal key block) skips it.
+  const int r_lo = max(r_begin, (int)wg.z * p.split_len), r_hi = min(p.N, (int)wg.z * p.split_len + p.split_len);
+  if (p.split > 1 && r_lo >= r_hi) return;
+  const int ntiles = r_hi > r_lo ? (r_hi - r_lo + TT - 1) / TT : 0;
   Chunk16 qreg[F32Stage<DP, NT>::NCH], greg[F32Stage<DP, NT>::NCH];
   float lreg = 0.f, loreg = 0.f, dreg = 0.f;
   auto gload = [&](int t0) {
@@ -392,13 +410,13 @@ void bwd_dkdv_kernel(const BwdParams p) {
     }
   };
   if (ntiles > 0) {
-    gload(r_begin);
+    gload(r_lo);
     sstore(0);
   }
   __syncthreads();
 
   for (int it = 0; it < ntiles; ++it) {
-    const int t0 = r_begin + it * TT, buf = it & 1;
+    const int t0 = r_lo + it * TT, buf = it & 1;
     const bool has_next = it + 1 < ntiles;
     if (has_next) gload(t0 + TT);
     f32x16 s = f32x16{}, dp = f32x16{};
@@ -452,6 +470,20 @@ void bwd_dkdv_kernel(const BwdParams p) {
     __syncthreads();
   }
   if (!key_ok) return;
+  if (p.split > 1) {  // this row range's unscaled dK and dV: the combine sums the ranges and scales dK
+    const int64_t o = (((int64_t)wg.z * p.BH + bh) * p.N + my_key) * p.dp;
+    float* dkp = p.part + p.part_stride + o;
+    float* dvp = p.part + 2 * p.part_stride + o;
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = dt * 32 + drow(r, g);
+        dkp[d] = dk[dt][r];
+        dvp[d] = dv[dt][r];
+      }
+    return;
+  }
   T* okp = static_cast<T*>(p.dk) + bi * p.dks[0] + hi * p.dks[1] + (int64_t)my_key * p.dks[2];
   T* ovp = static_cast<T*>(p.dv) + bi * p.dvs[0] + hi * p.dvs[1] + (int64_t)my_key * p.dvs[2];
 #pragma unroll
@@ -1479,10 +1511,16 @@ hipError_t launch_zero_fill(float* dst, int64_t n, hipStream_t st) {
 
 // ------------------------------------------------------------------ split backward
 int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias) {
-  if (dtype == ELSA_F32 || bias || dp > 64) return 1;
-  const int64_t wgs = bh * ((n + 127) / 128);  // the unsplit 4-wave grid
+  if (bias || dp > 64) return 1;
+  const int64_t wgs = bh * ((n + 127) / 128);  // the unsplit 4-wave grid (fp32's kernels too)
   int s = 1;
-  while (s < 8 && wgs * s < 512 && n / (2 * s) >= 256) s *= 2;
+  if (dtype == ELSA_F32) {
+    // fp32 stops where a doubling would pass one round of 512 work-groups: B8 H3 N1025 backward
+    // 0.344 ms unsplit, 0.394 ms in 4 ranges (864 work-groups); B1 H8 1K 0.331 -> 0.118 ms in 4
+    while (s < 8 && wgs * s * 2 <= 512 && n / (2 * s) >= 256) s *= 2;
+  } else {
+    while (s < 8 && wgs * s < 512 && n / (2 * s) >= 256) s *= 2;
+  }
   return s;
 }
 
@@ -1738,14 +1776,28 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
       e = hipGetLastError();
     }
   } else {
-    const dim3 grid((p.N + 32 * W - 1) / (32 * W), p.BH);
+    // fp32: the key (dq) and row (dK/dV) loops split over grid z for under-filled grids, as above
+    const dim3 grid((p.N + 32 * W - 1) / (32 * W), p.BH, (unsigned)(p.split > 1 ? p.split : 1));
+    const int kq = p.causal ? 1 : 0, kkv = p.causal ? 2 : 0;
+    const CombineOut cq{p.part, p.dq, {p.dqs[0], p.dqs[1], p.dqs[2]}, p.scale, kq};
+    const CombineOut ck{p.part + p.part_stride, p.dk, {p.dks[0], p.dks[1], p.dks[2]}, p.scale, kkv};
+    const CombineOut cv{p.part + 2 * p.part_stride, p.dv, {p.dvs[0], p.dvs[1], p.dvs[2]}, 1.f, kkv};
     if (stage < 0 || stage == 1) {
       hipLaunchKernelGGL((bwd_dq_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
       if ((e = hipGetLastError()) != hipSuccess) return e;
+      if (p.split > 1 && stage == 1 && (e = combine_launch<T>(p, &cq, 1, st)) != hipSuccess) return e;
     }
     if (stage < 0 || stage == 2) {
       hipLaunchKernelGGL((bwd_dkdv_kernel<T, DP, W, B>), grid, dim3(64 * W), 0, st, p);
-      e = hipGetLastError();
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      if (p.split > 1 && stage == 2) {
+        const CombineOut kv[2] = {ck, cv};
+        e = combine_launch<T>(p, kv, 2, st);
+      }
+    }
+    if (p.split > 1 && stage < 0) {
+      const CombineOut all[3] = {cq, ck, cv};
+      e = combine_launch<T>(p, all, 3, st);
     }
   }
   return e;

@@ -118,7 +118,7 @@ struct BwdParams {
   float scale_log2;  // scale * log2(e)
   // element strides (batch, head, row) of q, k, v, out, dout and of dq, dk, dv
   int64_t qs[3], ks[3], vs[3], os[3], gs[3], dqs[3], dks[3], dvs[3];
-  // split > 1 (bwd_splits): the fp16/bf16 dq and dK/dV kernels cut their key (dq) or row (dK/dV)
+  // split > 1 (bwd_splits): the 4-wave dq and dK/dV kernels cut their key (dq) or row (dK/dV)
   // loop into `split` ranges of split_len (a multiple of 64) over grid z, and write unscaled fp32
   // partials, [split][BH][N][dp] each for dq, dK and dV from part on; a combine kernel sums them
   int split, split_len, dp;
@@ -126,13 +126,12 @@ struct BwdParams {
   int64_t part_stride;  // floats from the dq partials to the dK ones and from those to the dV ones
 };
 
-// Ranges the fp16/bf16 backward cuts its loops into when its unsplit grid (128 rows or keys per
-// work-group) leaves the chip under-filled: 1 (no split) unless fewer than 512 work-groups, then
-// doubled while that stays short of 512 and n / (2 * split) is at least 256.  Each range is
+// Ranges the backward (fp16, bf16 and fp32) cuts its loops into when its unsplit grid (128 rows or
+// keys per work-group) leaves the chip under-filled: 1 (no split) unless fewer than 512 work-groups,
+// then doubled while that stays short of 512 and n / (2 * split) is at least 256.  Each range is
 // split_len = ceil(n / split) rounded up to whole 64-row stages, so the last one can be shorter
 // (B8 H3 N1025: 320, 320, 320 and 65 rows); the launch lasts as long as the longest range,
-// which no choice of whole-stage ranges makes shorter.  fp32, biased calls and head dims above
-// 64 keep 1.
+// which no choice of whole-stage ranges makes shorter.  Biased calls and head dims above 64 keep 1.
 int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias);
 
 // stage < 0: preprocess, dq and dk/dv; 0: preprocess only; 1: dq only; 2: dk/dv only.

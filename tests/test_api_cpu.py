@@ -378,8 +378,9 @@ def _align256(x):
     (2305, (8, 3), _lib.ELSA_F16, 32, 2),
     (16384, (1, 8), _lib.ELSA_F16, 64, 1),   # the north star's grid is full
     (197, (8, 3), _lib.ELSA_F16, 64, 1),     # ranges would fall below 256 rows
-    (1024, (1, 8), _lib.ELSA_F32, 64, 1),    # fp32 and d = 128 keep their unsplit kernels
-    (1024, (1, 8), _lib.ELSA_F16, 128, 1),
+    (1024, (1, 8), _lib.ELSA_F32, 64, 4),    # fp32 splits as fp16 does (its 4-wave kernels take 128 rows too)
+    (4096, (1, 8), _lib.ELSA_F32, 64, 2),
+    (1024, (1, 8), _lib.ELSA_F16, 128, 1),   # d = 128 keeps its unsplit kernels
 ])
 def test_bwd_workspace_holds_the_split_partials(n, bh, dtype, d, split):
     """Short sequences with few heads cut the backward's key (dq) and row (dK/dV) loops into ranges
