@@ -97,6 +97,14 @@ int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
     // 3% from 1 to 8 partitions
     int64_t p = cdiv(1024, q_tiles);
     p = std::min<int64_t>(p, std::max<int64_t>(1, n / 512));
+    // fp32: its fold spends 16 times longer per key than fp16's, so short partitions cost little
+    // and the grid's fill decides: where the rule above leaves fewer than 256 work-groups,
+    // partitions down to 64 keys until about 512.  Forward ms (Phase 1 + Phase 2, d64): B1 H8 1K
+    // 0.050 -> 0.029 (2 -> 8 partitions), causal 1K 0.051 -> 0.029, B8 H3 N197 0.024 -> 0.015 (1 ->
+    // 3), B1 H8 N512 0.047 -> 0.014 (1 -> 8); B8 H3 N1025 (432 work-groups) keeps 2 partitions
+    // (0.086 against 0.089 ms with 3)
+    if (a->dtype == ELSA_F32 && q_tiles * p < 256)
+      p = std::max<int64_t>(p, std::min<int64_t>(cdiv(512, q_tiles), std::max<int64_t>(1, n / 64)));
     if (n >= 8192) p = std::max<int64_t>(p, 2);
     // causal from 8K keys: partitions of n/4 keys within [2048, 8192].  About half of the
     // causal workgroups have no keys to fold; Phase 1 dispatches the rest longest first.

@@ -133,6 +133,18 @@ def test_plan_ping_pong_rule_only_where_the_ping_pong_fold_runs():
     assert rc == 0 and (p.partitions, p.partition_len) == (16, 512)
 
 
+# fp32 grids the 1024-workgroup rule leaves under 256 work-groups take partitions down to 64 keys
+# until about 512 (measured: B1 H8 1K 0.050 -> 0.029 ms, B8 H3 N197 0.024 -> 0.015 ms); larger ones keep it
+@pytest.mark.parametrize("n,bh,causal,parts,part", [
+    (1024, (1, 8), 0, 8, 128), (1024, (1, 8), 1, 8, 128), (197, (8, 3), 0, 3, 96), (512, (1, 8), 0, 8, 64),
+    (1025, (8, 3), 0, 2, 544),   # 432 work-groups already: two partitions (0.086 against 0.089 ms with three)
+    (2048, (1, 8), 0, 4, 512), (4096, (1, 8), 0, 4, 1024),
+])
+def test_plan_fp32_fills_short_grids(n, bh, causal, parts, part):
+    rc, p = _plan(_args(n=n, bh=bh, dtype=_lib.ELSA_F32, causal=causal))
+    assert rc == 0 and (p.partitions, p.partition_len) == (parts, part) and p.block_m == 128
+
+
 @pytest.mark.parametrize("n,bh,d", [(49, (8, 3), 32), (197, (8, 3), 64), (1024, (1, 8), 64), (65536, (1, 8), 64),
                                     (4097, (8, 3), 64), (300, (1, 2), 128)])
 def test_plan_partitions_cover_sequence(n, bh, d):
