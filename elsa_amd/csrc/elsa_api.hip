@@ -105,6 +105,13 @@ int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
     // (0.086 against 0.089 ms with 3)
     if (a->dtype == ELSA_F32 && q_tiles * p < 256)
       p = std::max<int64_t>(p, std::min<int64_t>(cdiv(512, q_tiles), std::max<int64_t>(1, n / 64)));
+    // fp16/bf16 grids at d <= 64 from 512 keys under 192 work-groups (a few heads of at most 2K rows):
+    // partitions down to 128 keys until about 256 work-groups.  Forward ms (fp16 d64): B1 H8 1K 0.012
+    // -> 0.010 (2 -> 4 partitions), N512 0.0099 -> 0.0084 (1 -> 4), causal N1025 0.0139 -> 0.0121
+    // (3 -> 5); B8 H3 N1025 (240 work-groups) keeps its two (5: 0.026 against 0.021 ms), and shorter
+    // sequences their one fused partition (B8 H3 N197: more measured slower)
+    if (a->dtype != ELSA_F32 && dp <= 64 && n >= 512 && q_tiles * p < 192)
+      p = std::max<int64_t>(p, std::min<int64_t>(cdiv(256, q_tiles), std::max<int64_t>(1, n / 128)));
     if (n >= 8192) p = std::max<int64_t>(p, 2);
     // causal from 8K keys: partitions of n/4 keys within [2048, 8192].  About half of the
     // causal workgroups have no keys to fold; Phase 1 dispatches the rest longest first.

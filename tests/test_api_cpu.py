@@ -145,6 +145,19 @@ def test_plan_fp32_fills_short_grids(n, bh, causal, parts, part):
     assert rc == 0 and (p.partitions, p.partition_len) == (parts, part) and p.block_m == 128
 
 
+# fp16/bf16 at d <= 64 under 192 work-groups: partitions down to 128 keys until about 256 work-groups
+@pytest.mark.parametrize("n,bh,dtype,causal,parts,part", [
+    (1024, (1, 8), _lib.ELSA_F16, 0, 4, 256), (1024, (1, 8), _lib.ELSA_BF16, 0, 4, 256),
+    (512, (1, 8), _lib.ELSA_F16, 0, 4, 128),
+    (197, (8, 3), _lib.ELSA_F16, 0, 1, 197),    # ViT-T 224 px keeps its one fused partition
+    (1025, (8, 3), _lib.ELSA_F16, 0, 2, 576),   # 240 work-groups: unchanged
+    (2048, (1, 8), _lib.ELSA_F16, 0, 4, 512),
+])
+def test_plan_short_16bit_grids_fill_to_256(n, bh, dtype, causal, parts, part):
+    rc, p = _plan(_args(n=n, bh=bh, dtype=dtype, causal=causal))
+    assert rc == 0 and (p.partitions, p.partition_len) == (parts, part)
+
+
 @pytest.mark.parametrize("n,bh,d", [(49, (8, 3), 32), (197, (8, 3), 64), (1024, (1, 8), 64), (65536, (1, 8), 64),
                                     (4097, (8, 3), 64), (300, (1, 2), 128)])
 def test_plan_partitions_cover_sequence(n, bh, d):
@@ -163,7 +176,11 @@ def test_plan_causal_partitions_of_a_quarter_within_2k_8k_from_8k(n, part, parts
 
 
 def test_plan_causal_short_partitions_round_to_the_nearest_row_block():
+    # B1 H8 causal 1025: a short grid (72 row blocks) takes 4 partitions of ceil(1025 / 4) = 257 keys,
+    # rounded to the nearest 128-row block: 256 keys, so 5 partitions, the last of one key
     rc, p = _plan(_args(n=1025, causal=1))
+    assert rc == 0 and p.block_m == 128 and p.partition_len == 256 and p.partitions == 5
+    rc, p = _plan(_args(n=1025, bh=(8, 3), causal=1))  # 216 row blocks: 2 partitions of 513 -> 512
     assert rc == 0 and p.block_m == 128 and p.partition_len == 512 and p.partitions == 3
 
 
