@@ -1511,16 +1511,15 @@ hipError_t launch_zero_fill(float* dst, int64_t n, hipStream_t st) {
 
 // ------------------------------------------------------------------ split backward
 int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias) {
+  (void)dtype;  // fp16, bf16 and fp32 alike: their 4-wave kernels take 128 rows or keys per work-group
   if (bias || dp > 64) return 1;
-  const int64_t wgs = bh * ((n + 127) / 128);  // the unsplit 4-wave grid (fp32's kernels too)
+  const int64_t wgs = bh * ((n + 127) / 128);  // the unsplit 4-wave grid
+  // double while the doubled grid stays within one round of 512 work-groups (two per CU): whole
+  // backward, fp16 d64, against doubling while the grid was short of 512: B8 H3 N1025 0.083 ->
+  // 0.065 ms (4 -> 2 ranges), causal 0.073 -> 0.057, B8 H3 N2305 0.188 -> 0.170 (2 -> 1), causal
+  // 0.150 -> 0.119, B16 H3 N1025 0.115 -> 0.087 (2 -> 1); fp32 B8 H3 N1025 0.394 -> 0.339 ms
   int s = 1;
-  if (dtype == ELSA_F32) {
-    // fp32 stops where a doubling would pass one round of 512 work-groups: B8 H3 N1025 backward
-    // 0.344 ms unsplit, 0.394 ms in 4 ranges (864 work-groups); B1 H8 1K 0.331 -> 0.118 ms in 4
-    while (s < 8 && wgs * s * 2 <= 512 && n / (2 * s) >= 256) s *= 2;
-  } else {
-    while (s < 8 && wgs * s < 512 && n / (2 * s) >= 256) s *= 2;
-  }
+  while (s < 8 && wgs * s * 2 <= 512 && n / (2 * s) >= 256) s *= 2;
   return s;
 }
 

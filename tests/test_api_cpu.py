@@ -403,8 +403,8 @@ def _align256(x):
     (1024, (1, 8), _lib.ELSA_F16, 64, 4),    # 64 four-wave work-groups: four 256-row ranges
     (4096, (1, 8), _lib.ELSA_F16, 64, 2),    # 256 work-groups: two ranges fill the chip twice
     (2048, (1, 8), _lib.ELSA_BF16, 64, 4),
-    (1025, (8, 3), _lib.ELSA_F16, 64, 4),    # ViT-T at 512 px
-    (2305, (8, 3), _lib.ELSA_F16, 32, 2),
+    (1025, (8, 3), _lib.ELSA_F16, 64, 2),    # ViT-T at 512 px: 216 work-groups, doubled once (432)
+    (2305, (8, 3), _lib.ELSA_F16, 32, 1),    # 456 work-groups: a doubling would pass one round of 512
     (16384, (1, 8), _lib.ELSA_F16, 64, 1),   # the north star's grid is full
     (197, (8, 3), _lib.ELSA_F16, 64, 1),     # ranges would fall below 256 rows
     (1024, (1, 8), _lib.ELSA_F32, 64, 4),    # fp32 splits as fp16 does (its 4-wave kernels take 128 rows too)
