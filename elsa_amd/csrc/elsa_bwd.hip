@@ -1703,10 +1703,16 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
         // 0.427 -> 0.605 ms, B4 H8 8K 0.457 -> 0.555 ms and B8 H3 N16385 (792) 1.25 -> 1.37 ms
         const dim3 grid8((p.N + 511) / 512, p.BH);
         const int64_t n8 = (int64_t)grid8.x * grid8.y;
-        wide = (int64_t)grid2.x * grid2.y >= 512 && (!p.causal || (DP == 64 && p.N >= 16384 && n8 % 512 == 0));
+        // non-causal D = 64 also where the 512-row work-groups take fewer rounds of the chip (256 at
+        // one per CU) than the 128-row ones (512 at two per CU): B8 H3 N4097 dq 0.190 -> 0.170 ms
+        // (792 work-groups, 2 rounds, against 216, 1); with the rounds level, B1 H8 8K 0.206 -> 0.282 ms
+        const int64_t g1 = (int64_t)((p.N + 127) / 128) * p.BH;
+        const bool fewer_rounds = DP == 64 && !p.causal && (g1 + 511) / 512 > (n8 + 255) / 256;
+        wide = ((int64_t)grid2.x * grid2.y >= 512 && (!p.causal || (DP == 64 && p.N >= 16384 && n8 % 512 == 0))) ||
+               fewer_rounds;
         bool w8 = false;
         if constexpr (DP == 64) {
-          if (wide && n8 >= 256) {
+          if (wide && (n8 >= 256 || fewer_rounds)) {
             // LDS-direct staging where every head dim chunk is data (D = 64) and the buffer ranges of
             // N rows of K and V stay below 2^31 bytes
             if (ld_kv) {
@@ -1746,11 +1752,13 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
     if (stage < 0 || stage == 2) {
       // dK/dV in 8-wave work-groups (256 keys) at D = 64 where that grid still puts two
       // work-groups on every CU: 16K 1.109 -> 1.078 ms, causal 16K 0.602 -> 0.569 ms, bf16 16K
-      // 1.053 -> 1.028 ms; at 4K (128 work-groups) 0.101 against 0.130 ms, so smaller grids keep 4
+      // 1.053 -> 1.028 ms; at 4K (128 work-groups) 0.101 against 0.130 ms, so smaller grids keep 4.
+      // Non-causal grids of 256-511 work-groups (one round at one per CU) take 8 too: dK/dV B8 H3
+      // N4097 0.290 -> 0.278 ms, B1 H8 8K 0.267 -> 0.261 ms, B2 H8 4K 0.138 -> 0.136 ms
       bool w8 = false;
       if constexpr (DP == 64) {
         const dim3 g8((p.N + 255) / 256, p.BH);
-        if ((int64_t)g8.x * g8.y >= 512) {
+        if ((int64_t)g8.x * g8.y >= (p.causal ? 512 : 256)) {
           // LDS-direct staging where every head dim chunk is data (D = 64) and the buffer ranges of
           // N rows of Q and dO stay below 2^31 bytes
           if constexpr (!B) {
