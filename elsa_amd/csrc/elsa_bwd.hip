@@ -1511,15 +1511,18 @@ hipError_t launch_zero_fill(float* dst, int64_t n, hipStream_t st) {
 
 // ------------------------------------------------------------------ split backward
 int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias) {
-  (void)dtype;  // fp16, bf16 and fp32 alike: their 4-wave kernels take 128 rows or keys per work-group
   if (bias || dp > 64) return 1;
   const int64_t wgs = bh * ((n + 127) / 128);  // the unsplit 4-wave grid
   // double while the doubled grid stays within one round of 512 work-groups (two per CU): whole
   // backward, fp16 d64, against doubling while the grid was short of 512: B8 H3 N1025 0.083 ->
   // 0.065 ms (4 -> 2 ranges), causal 0.073 -> 0.057, B8 H3 N2305 0.188 -> 0.170 (2 -> 1), causal
-  // 0.150 -> 0.119, B16 H3 N1025 0.115 -> 0.087 (2 -> 1); fp32 B8 H3 N1025 0.394 -> 0.339 ms
+  // 0.150 -> 0.119, B16 H3 N1025 0.115 -> 0.087 (2 -> 1); fp32 B8 H3 N1025 0.394 -> 0.339 ms.
+  // Ranges stay at least 256 keys or rows for fp16 and bf16 (128: B1 H8 N1024 0.038 -> 0.044 ms)
+  // and 64 for fp32, whose stages take several times longer (against 256: B8 H3 N197 0.089 ->
+  // 0.064 ms, B1 H8 N512 0.103 -> 0.061, B2 H3 N300 0.118 -> 0.064; 128 gave 0.089, 0.069, 0.082)
+  const int64_t min_range = dtype == ELSA_F32 ? 64 : 256;
   int s = 1;
-  while (s < 8 && wgs * s * 2 <= 512 && n / (2 * s) >= 256) s *= 2;
+  while (s < 8 && wgs * s * 2 <= 512 && n / (2 * s) >= min_range) s *= 2;
   return s;
 }
 

@@ -407,8 +407,11 @@ def _align256(x):
     (2305, (8, 3), _lib.ELSA_F16, 32, 1),    # 456 work-groups: a doubling would pass one round of 512
     (16384, (1, 8), _lib.ELSA_F16, 64, 1),   # the north star's grid is full
     (197, (8, 3), _lib.ELSA_F16, 64, 1),     # ranges would fall below 256 rows
-    (1024, (1, 8), _lib.ELSA_F32, 64, 4),    # fp32 splits as fp16 does (its 4-wave kernels take 128 rows too)
+    (1024, (1, 8), _lib.ELSA_F32, 64, 8),    # fp32 takes 128-row ranges where fp16 stops at 256
     (4096, (1, 8), _lib.ELSA_F32, 64, 2),
+    (197, (8, 3), _lib.ELSA_F32, 64, 2),     # fp32 ranges go down to 64 rows: 99 -> two stages of 64
+    (512, (1, 8), _lib.ELSA_F32, 64, 8),     # eight 64-row ranges
+    (300, (2, 3), _lib.ELSA_F32, 64, 4),     # 75 rows each; eight would fall below 64
     (1024, (1, 8), _lib.ELSA_F16, 128, 1),   # d = 128 keeps its unsplit kernels
 ])
 def test_bwd_workspace_holds_the_split_partials(n, bh, dtype, d, split):
