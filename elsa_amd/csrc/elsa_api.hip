@@ -416,7 +416,7 @@ elsa::BwdParams bwd_params(const elsa_bwd_args* a) {
   p.lse_row = reinterpret_cast<float*>(base + align256(rows * 4));
   p.lse_lo = reinterpret_cast<float*>(base + 2 * align256(rows * 4));
   p.dp = elsa::pad_head_dim(a->head_dim);
-  p.split = elsa::bwd_splits(a->dtype, p.dp, p.BH, p.N, a->bias.ptr != nullptr);
+  p.split = elsa::bwd_splits(a->dtype, p.dp, p.BH, p.N, a->bias.ptr != nullptr, a->is_causal != 0);
   // rows (dK/dV) or keys (dq) per range: whole 64-row stages
   p.split_len = p.split > 1 ? (int)((((int64_t)p.N + p.split - 1) / p.split + 63) / 64 * 64) : p.N;
   p.part = p.split > 1 ? reinterpret_cast<float*>(base + 3 * align256(rows * 4)) : nullptr;
@@ -560,7 +560,8 @@ int elsa_phase2(const elsa_fwd_args* a, int32_t q_start, int32_t q_len, void* st
 // fp32 partials of a split backward (dq, dK, dV): split * rows * dp floats each
 static size_t bwd_part_bytes(const elsa_bwd_args* a) {
   const int dp = elsa::pad_head_dim(a->head_dim);
-  const int split = elsa::bwd_splits(a->dtype, dp, (int64_t)a->batch * a->heads, a->seq_len, a->bias.ptr != nullptr);
+  const int split = elsa::bwd_splits(a->dtype, dp, (int64_t)a->batch * a->heads, a->seq_len, a->bias.ptr != nullptr,
+                                     a->is_causal != 0);
   if (split <= 1) return 0;
   const size_t rows = (size_t)a->batch * a->heads * a->seq_len;
   return 3 * align256((size_t)split * rows * dp * 4);

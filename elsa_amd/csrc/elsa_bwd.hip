@@ -1510,7 +1510,17 @@ hipError_t launch_zero_fill(float* dst, int64_t n, hipStream_t st) {
 }
 
 // ------------------------------------------------------------------ split backward
-int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias) {
+// Work-groups of a causal backward split into s ranges that hold work: a 128-row block's dq covers
+// the keys below k_end = min(n, 128 * (block + 1)), so its ranges from ceil(k_end / split_len) on
+// return at once (the dK/dV grid mirrors this count).
+static int64_t causal_live_wgs(int64_t bh, int64_t n, int s) {
+  const int64_t len = ((n + s - 1) / s + 63) / 64 * 64;
+  int64_t live = 0;
+  for (int64_t b0 = 0; b0 < n; b0 += 128) live += (std::min(n, b0 + 128) + len - 1) / len;
+  return bh * live;
+}
+
+int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias, bool causal) {
   if (bias || dp > 64) return 1;
   const int64_t wgs = bh * ((n + 127) / 128);  // the unsplit 4-wave grid
   // double while the doubled grid stays within one round of 512 work-groups (two per CU): whole
@@ -1520,9 +1530,18 @@ int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias) {
   // Ranges stay at least 256 keys or rows for fp16 and bf16 (128: B1 H8 N1024 0.038 -> 0.044 ms)
   // and 64 for fp32, whose stages take several times longer (against 256: B8 H3 N197 0.089 ->
   // 0.064 ms, B1 H8 N512 0.103 -> 0.061, B2 H3 N300 0.118 -> 0.064; 128 gave 0.089, 0.069, 0.082)
+  // Causal fp32 calls count only the work-groups that hold work (the others return at once): the
+  // doubling splits the longest rows' key ranges, and an fp32 stage is long enough that those set
+  // the time.  Against the count of every work-group: B1 H8 N1025 0.202 -> 0.162 ms (4 -> 8 ranges),
+  // B2 H8 N2049 0.895 -> 0.571 (1 -> 2), B1 H8 N4097 1.305 -> 1.098, N5000 1.773 -> 1.333, N3000
+  // 0.800 -> 0.723 (2 -> 4).  fp16 went both ways (B2 H8 N2049 0.103 -> 0.085 ms, but B1 H12 N2048
+  // 0.076 -> 0.083 and B1 H8 N5000 0.169 -> 0.177), so 16-bit calls count every work-group.
   const int64_t min_range = dtype == ELSA_F32 ? 64 : 256;
+  const bool live_only = causal && dtype == ELSA_F32 && wgs <= 512;
   int s = 1;
-  while (s < 8 && wgs * s * 2 <= 512 && n / (2 * s) >= min_range) s *= 2;
+  while (s < 8 && n / (2 * s) >= min_range &&
+         (wgs * s * 2 <= 512 || (live_only && causal_live_wgs(bh, n, 2 * s) <= 512)))
+    s *= 2;
   return s;
 }
 

@@ -128,12 +128,13 @@ struct BwdParams {
 
 // Ranges the backward (fp16, bf16 and fp32) cuts its loops into when its unsplit grid (128 rows or
 // keys per work-group) leaves the chip under-filled: doubled from 1 while the doubled grid stays
-// within 512 work-groups and n / (2 * split) is at least 256 (64 for fp32).  Each range is
+// within 512 work-groups (causal fp32: 512 that hold work) and n / (2 * split) is at least 256 (64
+// for fp32).  Each range is
 // split_len = ceil(n / split) rounded up to whole 64-row stages, so the last one can be shorter
 // (B1 H4 N2049: 576, 576, 576 and 321 rows) or start past n (B1 H2 N2049: 8 ranges of 320, the last
 // from 2240); the launch lasts as long as the longest range,
 // which no choice of whole-stage ranges makes shorter.  Biased calls and head dims above 64 keep 1.
-int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias);
+int bwd_splits(int dtype, int dp, int64_t bh, int64_t n, bool bias, bool causal);
 
 // stage < 0: preprocess, dq and dk/dv; 0: preprocess only; 1: dq only; 2: dk/dv only.
 hipError_t launch_bwd(const BwdParams& p, int dtype, int stage, hipStream_t stream);

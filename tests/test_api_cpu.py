@@ -427,3 +427,33 @@ def test_bwd_workspace_holds_the_split_partials(n, bh, dtype, d, split):
     bias = torch.zeros(1)
     b.bias = _lib.bias_desc(bias, (0, 0, n, 1))
     assert lib.elsa_bwd_workspace_bytes(ctypes.byref(b)) == 3 * _align256(rows * 4)
+
+
+def _causal_live_wgs(bh, n, s):
+    # work-groups of a causal split that hold work: a 128-row block's dq ranges stop at its last row
+    sl = ((n + s - 1) // s + 63) // 64 * 64
+    return bh * sum((min(n, b0 + 128) + sl - 1) // sl for b0 in range(0, n, 128))
+
+
+@pytest.mark.parametrize("n,bh,dtype,causal,split", [
+    (4097, (1, 8), _lib.ELSA_F32, True, 2),    # 264 work-groups, 400 of 528 hold work once doubled
+    (2049, (2, 8), _lib.ELSA_F32, True, 2),
+    (1025, (1, 8), _lib.ELSA_F32, True, 8),    # 8 ranges of 192 keys: 256 of 576 hold work
+    (1025, (1, 8), _lib.ELSA_F32, False, 4),   # non-causal: every work-group counts
+    (3000, (1, 8), _lib.ELSA_F32, True, 4),
+    (8192, (1, 8), _lib.ELSA_F32, True, 1),    # 512 work-groups fill the round already
+    (4097, (1, 8), _lib.ELSA_F16, True, 1),    # 16-bit calls count every work-group
+    (2049, (2, 8), _lib.ELSA_BF16, True, 1),
+])
+def test_causal_fp32_split_counts_the_work_groups_that_hold_work(n, bh, dtype, causal, split):
+    """Causal fp32 backward: the split doubles while the work-groups that hold work (the others return
+    at once) fit one round of 512; 16-bit and non-causal calls count every work-group."""
+    lib = _lib.load()
+    b = _lib.BwdArgs()
+    b.batch, b.heads, b.seq_len, b.head_dim, b.dtype, b.is_causal = bh[0], bh[1], n, 64, dtype, int(causal)
+    rows = bh[0] * bh[1] * n
+    part = 3 * _align256(split * rows * 64 * 4) if split > 1 else 0
+    assert lib.elsa_bwd_workspace_bytes(ctypes.byref(b)) == 3 * _align256(rows * 4) + part
+    if causal and dtype == _lib.ELSA_F32 and split > 1:
+        assert _causal_live_wgs(bh[0] * bh[1], n, split) <= 512
+        assert split == 8 or n // (2 * split) < 64 or _causal_live_wgs(bh[0] * bh[1], n, 2 * split) > 512

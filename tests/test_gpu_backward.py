@@ -39,6 +39,7 @@ CASES = [
     ((1, 4, 2049, 64), "fp16", False),  # 4 ranges of 576, the last of 321 rows
     ((1, 2, 300, 128), "fp16", False),
     ((1, 2, 300, 128), "fp32", True),
+    ((1, 8, 1025, 64), "fp32", True),   # 8 ranges of 192 keys: 256 of the 576 work-groups hold work
     ((1, 3, 197, 64), "bf16", False),
     ((1, 2, 90, 40), "fp32", False),
     ((2, 3, 49, 32), "bf16", True),     # 2-wave work-groups: at most 64 rows, head dims up to 32
@@ -534,12 +535,16 @@ def test_backward_stages_one_by_one_are_the_whole_backward(shape, dt, causal):
 # combine skips those ranges and any range that starts past N.  With the workspace filled with NaN
 # first, a partial read that no work-group wrote shows up in the gradients, and so does a row's D or
 # LSE2 that the dq kernels (the preprocess at d = 64) left unwritten for the dK/dV kernel.
-@pytest.mark.parametrize("shape,causal", [((1, 2, 2049, 64), True), ((1, 2, 2049, 64), False),
-                                          ((1, 4, 2049, 64), True),
-                                          ((1, 8, 2048, 64), True), ((8, 3, 1025, 64), True),
-                                          ((1, 2, 4097, 64), True), ((1, 8, 16385, 64), False),
-                                          ((1, 8, 8192, 64), True)])
-def test_split_backward_reads_only_written_partials(shape, causal):
+@pytest.mark.parametrize("shape,causal,dt", [((1, 2, 2049, 64), True, "fp16"), ((1, 2, 2049, 64), False, "fp16"),
+                                             ((1, 4, 2049, 64), True, "fp16"),
+                                             ((1, 8, 2048, 64), True, "fp16"), ((8, 3, 1025, 64), True, "fp16"),
+                                             ((1, 2, 4097, 64), True, "fp16"), ((1, 8, 16385, 64), False, "fp16"),
+                                             ((1, 8, 8192, 64), True, "fp16"),
+                                             # fp32: ranges down to 64 rows, and causal splits that count
+                                             # only the work-groups holding work
+                                             ((1, 8, 1025, 64), True, "fp32"), ((2, 8, 2049, 64), True, "fp32"),
+                                             ((1, 8, 4097, 64), True, "fp32"), ((8, 3, 197, 64), False, "fp32")])
+def test_split_backward_reads_only_written_partials(shape, causal, dt):
     import ctypes
     import math
 
@@ -547,10 +552,10 @@ def test_split_backward_reads_only_written_partials(shape, causal):
     from elsa_amd.attention import _BiasMeta
     from elsa_amd.attention_bwd import _attach_workspace, _bwd_args
 
-    describe(f"split backward over a NaN workspace {shape} causal={causal}")
+    describe(f"split backward over a NaN workspace {shape} causal={causal} {dt}")
     lib = _lib.load()
     g = torch.Generator().manual_seed(32)
-    q, k, v, do = (torch.randn(shape, generator=g).half().cuda() for _ in range(4))
+    q, k, v, do = (torch.randn(shape, generator=g).to(TORCH_DT[dt]).cuda() for _ in range(4))
     out, rm, rz = elsa_amd.twopass_attention_with_state(q, k, v, is_causal=causal)
     want = elsa_amd.twopass_attention_backward(q, k, v, out, do, is_causal=causal, row_m=rm, row_z=rz)
     dq, dk, dv = (torch.full_like(x, float("nan")) for x in (q, k, v))
