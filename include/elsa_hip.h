@@ -136,8 +136,9 @@ typedef struct elsa_bwd_args {
   float scale;           /* softmax scale on q.k; 0 = 1/sqrt(head_dim)          */
   int32_t _pad;
   void* workspace;       /* elsa_bwd_workspace_bytes: 3*B*H*N floats (D, LSE2 and its low part),
-                          * and for short fp16/bf16 sequences with few heads the fp32 partials of
-                          * the split backward (3*split*B*H*N*dp floats, split <= 8)            */
+                          * and for short sequences with few heads the fp32 partials of the split
+                          * backward (3*split*B*H*N*dp floats, split <= 8).  The size depends on
+                          * the shape, dtype, head_dim, is_causal and bias fields: set them first */
   size_t workspace_bytes;
   /* zero = dense [B,H,N,D].  The reference backward reads contiguous copies
    * (attention_bwd.py:722-726); strided views avoid them. */
