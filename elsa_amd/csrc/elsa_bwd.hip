@@ -196,9 +196,11 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
   constexpr int TS1 = TT + 1;     // transposed K tile [DP][TS1]: conflict-free transposing writes
   constexpr int RS4 = DP + 4;     // row-major K and V tiles [TT][RS4]
   constexpr int NM = DP / 8;
-  __shared__ __attribute__((aligned(16))) float Kr[TT * RS4];
-  __shared__ __attribute__((aligned(16))) float Vr[TT * RS4];
-  __shared__ __attribute__((aligned(16))) float Kt[DP * TS1];
+  // two buffers: stage i + 1 goes from global memory into registers while stage i computes, and
+  // from there into the other buffer
+  __shared__ __attribute__((aligned(16))) float Kr[2][TT * RS4];
+  __shared__ __attribute__((aligned(16))) float Vr[2][TT * RS4];
+  __shared__ __attribute__((aligned(16))) float Kt[2][DP * TS1];
 
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, c = lane & 31,
             g = lane >> 5;
@@ -240,27 +242,47 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
   const int k_lo = min(k_end, (int)wg.z * p.split_len), k_hi = min(k_end, k_lo + p.split_len);
   if (p.split > 1 && k_lo >= k_hi) return;
   constexpr int CPR = DP / 4;  // 16-byte chunks per key row
-
-  for (int t0 = k_lo; t0 < k_hi; t0 += TT) {
-    __syncthreads();
-    for (int ci = tid; ci < TT * CPR; ci += NT) {  // keys >= k_hi and d >= D are zeros
-      const int r = ci / CPR, d0 = (ci % CPR) * 4, key = t0 + r;
-      f32x4 kv{}, vv{};
-      if (key < k_hi && d0 < p.D) {
-        kv = *reinterpret_cast<const f32x4*>(K + (int64_t)key * p.ks[2] + d0);
-        vv = *reinterpret_cast<const f32x4*>(V + (int64_t)key * p.vs[2] + d0);
-      }
-      *reinterpret_cast<f32x4*>(&Kr[r * RS4 + d0]) = kv;
-      *reinterpret_cast<f32x4*>(&Vr[r * RS4 + d0]) = vv;
+  constexpr int NCH = TT * CPR / NT;
+  static_assert((TT * CPR) % NT == 0, "staging must divide evenly");
+  // chunk tid + i NT of a stage: key row ci / CPR, head dims (ci % CPR) * 4 .. + 3; keys >= k_hi
+  // and d >= D are zeros
+  f32x4 kreg[NCH], vreg[NCH];
+  auto gload = [&](int t0) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) Kt[(d0 + u) * TS1 + r] = kv[u];
+    for (int i = 0; i < NCH; ++i) {
+      const int ci = tid + i * NT;
+      const int r = ci / CPR, d0 = (ci % CPR) * 4, key = t0 + r;
+      const bool ok = key < k_hi && d0 < p.D;
+      kreg[i] = ok ? *reinterpret_cast<const f32x4*>(K + (int64_t)key * p.ks[2] + d0) : f32x4{};
+      vreg[i] = ok ? *reinterpret_cast<const f32x4*>(V + (int64_t)key * p.vs[2] + d0) : f32x4{};
     }
-    __syncthreads();
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int ci = tid + i * NT;
+      const int r = ci / CPR, d0 = (ci % CPR) * 4;
+      *reinterpret_cast<f32x4*>(&Kr[buf][r * RS4 + d0]) = kreg[i];
+      *reinterpret_cast<f32x4*>(&Vr[buf][r * RS4 + d0]) = vreg[i];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) Kt[buf][(d0 + u) * TS1 + r] = kreg[i][u];
+    }
+  };
+  if (k_lo < k_hi) {
+    gload(k_lo);
+    sstore(0);
+  }
+  __syncthreads();
+
+  for (int t0 = k_lo, buf = 0; t0 < k_hi; t0 += TT, buf ^= 1) {
+    // buffer buf ^ 1 was last read by the previous stage, before the barrier that ended it
+    const bool has_next = t0 + TT < k_hi;
+    if (has_next) gload(t0 + TT);
     f32x16 s = f32x16{}, dp = f32x16{};
     {
       // A operands: stage key swap23(c), d = 8m + 4g .. + 3
-      const float* kr = Kr + swap23(c) * RS4 + 4 * g;
-      const float* vr = Vr + swap23(c) * RS4 + 4 * g;
+      const float* kr = Kr[buf] + swap23(c) * RS4 + 4 * g;
+      const float* vr = Vr[buf] + swap23(c) * RS4 + 4 * g;
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
         const f32x4 ka = *reinterpret_cast<const f32x4*>(kr + 8 * m);
@@ -295,13 +317,15 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
       const int k0 = 16 * (jb >> 1) + 8 * g + 4 * (jb & 1);  // key_of_reg(4 jb, g)
 #pragma unroll
       for (int dt = 0; dt < C::NDT; ++dt) {
-        const float* ka = Kt + (dt * 32 + c) * TS1 + k0;
+        const float* ka = Kt[buf] + (dt * 32 + c) * TS1 + k0;
 #pragma unroll
         for (int u = 0; u < 4; ++u) st[dt] = M::mma(ka[u], s[4 * jb + u], st[dt]);
       }
     }
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt) acc[dt] += st[dt];
+    if (has_next) sstore(buf ^ 1);
+    __syncthreads();
   }
   if (!row_ok) return;
   if (p.split > 1) {  // this key range's unscaled dQ: the combine sums the ranges and scales
