@@ -237,7 +237,7 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
   for (int dt = 0; dt < C::NDT; ++dt) acc[dt] = f32x16{};
   const int k_end = p.causal ? wg_last + 1 : p.N;
   // split (bwd_splits; 1 range of N keys otherwise): this work-group's keys [k_lo, k_hi) over grid z,
-  // whole 64-key ranges, so a stage never straddles a range end short of k_end.  An empty range
+  // whole 32-key stages, so a stage never straddles a range end short of k_end.  An empty range
   // writes no partial, and the combine (kind 0 past N, kind 1 past a causal row block) skips it.
   const int k_lo = min(k_end, (int)wg.z * p.split_len), k_hi = min(k_end, k_lo + p.split_len);
   if (p.split > 1 && k_lo >= k_hi) return;
@@ -407,7 +407,7 @@ void bwd_dkdv_kernel(const BwdParams p) {
   }
   const int r_begin = p.causal ? (wg_key0 / TT) * TT : 0;
   // split (bwd_splits; 1 range of N rows otherwise): this work-group's rows [r_lo, r_hi) over grid z,
-  // whole 64-row ranges.  An empty range writes no partial, and the combine (kind 0 past N, kind 2
+  // whole 32-row stages.  An empty range writes no partial, and the combine (kind 0 past N, kind 2
   // before a causal key block) skips it.
   const int r_lo = max(r_begin, (int)wg.z * p.split_len), r_hi = min(p.N, (int)wg.z * p.split_len + p.split_len);
   if (p.split > 1 && r_lo >= r_hi) return;
@@ -1538,7 +1538,7 @@ hipError_t launch_zero_fill(float* dst, int64_t n, hipStream_t st) {
 // the keys below k_end = min(n, 128 * (block + 1)), so its ranges from ceil(k_end / split_len) on
 // return at once (the dK/dV grid mirrors this count).
 static int64_t causal_live_wgs(int64_t bh, int64_t n, int s) {
-  const int64_t len = ((n + s - 1) / s + 63) / 64 * 64;
+  const int64_t len = ((n + s - 1) / s + 31) / 32 * 32;  // the fp32 split_len: whole 32-key stages
   int64_t live = 0;
   for (int64_t b0 = 0; b0 < n; b0 += 128) live += (std::min(n, b0 + 128) + len - 1) / len;
   return bh * live;

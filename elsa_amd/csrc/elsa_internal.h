@@ -119,7 +119,7 @@ struct BwdParams {
   // element strides (batch, head, row) of q, k, v, out, dout and of dq, dk, dv
   int64_t qs[3], ks[3], vs[3], os[3], gs[3], dqs[3], dks[3], dvs[3];
   // split > 1 (bwd_splits): the 4-wave dq and dK/dV kernels cut their key (dq) or row (dK/dV)
-  // loop into `split` ranges of split_len (a multiple of 64) over grid z, and write unscaled fp32
+  // loop into `split` ranges of split_len (a multiple of 64; of 32 for fp32) over grid z, and write unscaled fp32
   // partials, [split][BH][N][dp] each for dq, dK and dV from part on; a combine kernel sums them
   int split, split_len, dp;
   float* part;
@@ -130,7 +130,7 @@ struct BwdParams {
 // keys per work-group) leaves the chip under-filled: doubled from 1 while the doubled grid stays
 // within 512 work-groups (causal fp32: 512 that hold work) and n / (2 * split) is at least 256 (64
 // for fp32).  Each range is
-// split_len = ceil(n / split) rounded up to whole 64-row stages, so the last one can be shorter
+// split_len = ceil(n / split) rounded up to whole stages (64 rows; 32 for fp32), so the last one can be shorter
 // (B1 H4 N2049: 576, 576, 576 and 321 rows) or start past n (B1 H2 N2049: 8 ranges of 320, the last
 // from 2240); the launch lasts as long as the longest range,
 // which no choice of whole-stage ranges makes shorter.  Biased calls and head dims above 64 keep 1.

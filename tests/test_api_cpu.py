@@ -430,15 +430,16 @@ def test_bwd_workspace_holds_the_split_partials(n, bh, dtype, d, split):
 
 
 def _causal_live_wgs(bh, n, s):
-    # work-groups of a causal split that hold work: a 128-row block's dq ranges stop at its last row
-    sl = ((n + s - 1) // s + 63) // 64 * 64
+    # work-groups of a causal fp32 split that hold work: a 128-row block's dq ranges stop at its last
+    # row; fp32 ranges are whole 32-key stages
+    sl = ((n + s - 1) // s + 31) // 32 * 32
     return bh * sum((min(n, b0 + 128) + sl - 1) // sl for b0 in range(0, n, 128))
 
 
 @pytest.mark.parametrize("n,bh,dtype,causal,split", [
     (4097, (1, 8), _lib.ELSA_F32, True, 2),    # 264 work-groups, 400 of 528 hold work once doubled
     (2049, (2, 8), _lib.ELSA_F32, True, 2),
-    (1025, (1, 8), _lib.ELSA_F32, True, 8),    # 8 ranges of 192 keys: 256 of 576 hold work
+    (1025, (1, 8), _lib.ELSA_F32, True, 8),    # 8 ranges of 160 keys: 312 of 576 hold work
     (1025, (1, 8), _lib.ELSA_F32, False, 4),   # non-causal: every work-group counts
     (3000, (1, 8), _lib.ELSA_F32, True, 4),
     (8192, (1, 8), _lib.ELSA_F32, True, 1),    # 512 work-groups fill the round already

@@ -39,7 +39,7 @@ CASES = [
     ((1, 4, 2049, 64), "fp16", False),  # 4 ranges of 576, the last of 321 rows
     ((1, 2, 300, 128), "fp16", False),
     ((1, 2, 300, 128), "fp32", True),
-    ((1, 8, 1025, 64), "fp32", True),   # 8 ranges of 192 keys: 256 of the 576 work-groups hold work
+    ((1, 8, 1025, 64), "fp32", True),   # 8 ranges of 160 keys: 312 of the 576 work-groups hold work
     ((1, 3, 197, 64), "bf16", False),
     ((1, 2, 90, 40), "fp32", False),
     ((2, 3, 49, 32), "bf16", True),     # 2-wave work-groups: at most 64 rows, head dims up to 32
