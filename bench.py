@@ -210,9 +210,10 @@ def _kernel_ms(lib, stream, q, k, v, do, causal, block_n, steps):
     chunks = [(s_, min(qc, N - s_)) for s_ in range(0, N, qc)]
 
     fused = plan["partitions"] == 1
-    # fp16/bf16 at d = 64 (dense operands, N rows under 2 GiB): the dq kernels run the preprocess of
-    # their rows, and a whole backward (elsa_bwd) launches no preprocess kernel
-    pre_fused = q.dtype in (torch.float16, torch.bfloat16) and D == 64 and N * D * q.element_size() < 2**31
+    # fp16/bf16 at d = 64 (dense operands, N rows under 2 GiB) and fp32 at d <= 64: the dq kernels run
+    # the preprocess of their rows, and a whole backward (elsa_bwd) launches no preprocess kernel
+    pre_fused = ((q.dtype in (torch.float16, torch.bfloat16) and D == 64 and N * D * q.element_size() < 2**31)
+                 or (q.dtype == torch.float32 and D <= 64))
     # each launch set takes the stream handle it launches on
     launches = {
         "phase1_fold": ((lambda h: [lib.elsa_fwd(ctypes.byref(fa), h)]) if fused else

@@ -227,9 +227,47 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
     qf[m] = ok ? *reinterpret_cast<const f32x4*>(Q + (int64_t)rsafe * p.qs[2] + d0) : f32x4{};
     gf[m] = ok ? *reinterpret_cast<const f32x4*>(dO + (int64_t)rsafe * p.gs[2] + d0) : f32x4{};
   }
-  const float lse = row_ok ? p.lse_row[(int64_t)bh * p.N + my_row] : 0.f;
-  const float lse_lo = row_ok ? p.lse_lo[(int64_t)bh * p.N + my_row] : 0.f;
-  const float dd = row_ok ? p.d_row[(int64_t)bh * p.N + my_row] : 0.f;
+  float lse, lse_lo, dd;
+  const int64_t ri = (int64_t)bh * p.N + rsafe;
+  if constexpr (DP <= 64) {
+    // the preprocess of these rows, in bwd_pre_kernel's order: that kernel's lane j of a row chains
+    // fmas over the 4-float chunks j, j + 8, ... below D, and the 8 lanes' sums add pairwise,
+    // ((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7)).  Here chunk 2m + g is this lane's m-th
+    // load, so lane group g forms a_{2i+g} over m = i, i + 4, and lanes c and c + 32 add the pairs.
+    // The work-groups of the first key range store D and LSE2 for the dK/dV kernel, so a whole
+    // backward launches no preprocess.
+    const T* O = static_cast<const T*>(p.out) + bi * p.os[0] + hi * p.os[1] + (int64_t)rsafe * p.os[2];
+    float pair[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float a = 0.f;
+#pragma unroll
+      for (int m = i; m < NM; m += 4) {
+        const int d0 = 8 * m + 4 * g;
+        if (d0 < p.D) {
+          const f32x4 o4 = row_ok ? *reinterpret_cast<const f32x4*>(O + d0) : f32x4{};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) a = fmaf(o4[t], gf[m][t], a);
+        }
+      }
+      pair[i] = a + __shfl_xor(a, 32);
+    }
+    const float dsum = (pair[0] + pair[1]) + (pair[2] + pair[3]);
+    float lhi, llo;
+    lse2_split(p.row_m[ri], p.row_z[ri], lhi, llo);
+    if (row_ok && g == 0 && wg.z == 0) {
+      p.d_row[ri] = dsum;
+      p.lse_row[ri] = lhi;
+      p.lse_lo[ri] = llo;
+    }
+    lse = row_ok ? lhi : 0.f;
+    lse_lo = row_ok ? llo : 0.f;
+    dd = row_ok ? dsum : 0.f;
+  } else {
+    lse = row_ok ? p.lse_row[ri] : 0.f;
+    lse_lo = row_ok ? p.lse_lo[ri] : 0.f;
+    dd = row_ok ? p.d_row[ri] : 0.f;
+  }
   const bool live = row_ok && lse > kNegInf;
 
   f32x16 acc[C::NDT];
@@ -1685,7 +1723,9 @@ static hipError_t bwd_launch3(const BwdParams& p, int stage, hipStream_t st) {
                      (int64_t)p.N * p.vs[2] * es < lim;
   const bool ld_qg = sizeof(T) == 2 && !B && DP == 64 && p.D == 64 && (int64_t)p.N * p.qs[2] * es < lim &&
                      (int64_t)p.N * p.gs[2] * es < lim;
-  if (stage == 0 || (stage < 0 && !ld_kv)) {
+  // the fp32 dq kernels at D <= 64 run the preprocess of their rows too
+  const bool pre_in_dq = ld_kv || (sizeof(T) == 4 && DP <= 64);
+  if (stage == 0 || (stage < 0 && !pre_in_dq)) {
     if ((e = pre_launch<T>(p, st)) != hipSuccess) return e;
   }
   if constexpr (DP == 32) {
