@@ -378,9 +378,11 @@ __global__ __launch_bounds__(64 * WAVES) void bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int d = dt * 32 + drow(r, g);
-      if (d < p.D) out[d] = static_cast<T>(acc[dt][r] * p.scale);
+    for (int q4 = 0; q4 < 4; ++q4) {  // 16-byte stores, as in bwd_dkdv_kernel
+      const int d = dt * 32 + drow(4 * q4, g);
+      if (d < p.D)
+        *reinterpret_cast<f32x4*>(out + d) = f32x4{acc[dt][4 * q4] * p.scale, acc[dt][4 * q4 + 1] * p.scale,
+                                                   acc[dt][4 * q4 + 2] * p.scale, acc[dt][4 * q4 + 3] * p.scale};
     }
 }
 
@@ -532,6 +534,9 @@ void bwd_dkdv_kernel(const BwdParams p) {
     __syncthreads();
   }
   if (!key_ok) return;
+  // registers 4q .. 4q + 3 hold head dims dt * 32 + drow(4q, g) .. + 3: one 16-byte store each
+  // (pointers are 16-byte aligned and strides multiples of 8 elements; D is a multiple of 8, so a
+  // group starting below D ends below it)
   if (p.split > 1) {  // this row range's unscaled dK and dV: the combine sums the ranges and scales dK
     const int64_t o = (((int64_t)wg.z * p.BH + bh) * p.N + my_key) * p.dp;
     float* dkp = p.part + p.part_stride + o;
@@ -539,10 +544,12 @@ void bwd_dkdv_kernel(const BwdParams p) {
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int d = dt * 32 + drow(r, g);
-        dkp[d] = dk[dt][r];
-        dvp[d] = dv[dt][r];
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = dt * 32 + drow(4 * q4, g);
+        *reinterpret_cast<f32x4*>(dkp + d) =
+            f32x4{dk[dt][4 * q4], dk[dt][4 * q4 + 1], dk[dt][4 * q4 + 2], dk[dt][4 * q4 + 3]};
+        *reinterpret_cast<f32x4*>(dvp + d) =
+            f32x4{dv[dt][4 * q4], dv[dt][4 * q4 + 1], dv[dt][4 * q4 + 2], dv[dt][4 * q4 + 3]};
       }
     return;
   }
@@ -551,11 +558,13 @@ void bwd_dkdv_kernel(const BwdParams p) {
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int d = dt * 32 + drow(r, g);
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = dt * 32 + drow(4 * q4, g);
       if (d < p.D) {
-        okp[d] = static_cast<T>(dk[dt][r] * p.scale);
-        ovp[d] = static_cast<T>(dv[dt][r]);
+        *reinterpret_cast<f32x4*>(okp + d) = f32x4{dk[dt][4 * q4] * p.scale, dk[dt][4 * q4 + 1] * p.scale,
+                                                   dk[dt][4 * q4 + 2] * p.scale, dk[dt][4 * q4 + 3] * p.scale};
+        *reinterpret_cast<f32x4*>(ovp + d) =
+            f32x4{dv[dt][4 * q4], dv[dt][4 * q4 + 1], dv[dt][4 * q4 + 2], dv[dt][4 * q4 + 3]};
       }
     }
 }
