@@ -102,9 +102,12 @@ int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
     // partitions down to 64 keys until about 512.  Forward ms (Phase 1 + Phase 2, d64): B1 H8 1K
     // 0.050 -> 0.029 (2 -> 8 partitions), causal 1K 0.051 -> 0.029, B8 H3 N197 0.024 -> 0.015 (1 ->
     // 3), B1 H8 N512 0.047 -> 0.014 (1 -> 8); B8 H3 N1025 (432 work-groups) keeps 2 partitions
-    // (0.086 against 0.089 ms with 3)
+    // (0.086 against 0.089 ms with 3).  The count is capped at ceil(n / 64), not floor(n / 64): a
+    // short tail partition costs less than a third 32-key stage in every work-group: B8 H3 N197
+    // 0.0154 -> 0.0127 ms (3 -> 4 partitions), B2 H3 N300 0.0149 -> 0.0131, B1 H2 N90 0.0124 ->
+    // 0.0112 (1 -> 2)
     if (a->dtype == ELSA_F32 && q_tiles * p < 256)
-      p = std::max<int64_t>(p, std::min<int64_t>(cdiv(512, q_tiles), std::max<int64_t>(1, n / 64)));
+      p = std::max<int64_t>(p, std::min<int64_t>(cdiv(512, q_tiles), cdiv(n, 64)));
     // fp16/bf16 grids at d <= 64 from 512 keys under 192 work-groups (a few heads of at most 2K rows):
     // partitions down to 128 keys until about 256 work-groups.  Forward ms (fp16 d64): B1 H8 1K 0.012
     // -> 0.010 (2 -> 4 partitions), N512 0.0099 -> 0.0084 (1 -> 4), causal N1025 0.0139 -> 0.0121

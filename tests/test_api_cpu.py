@@ -134,9 +134,11 @@ def test_plan_ping_pong_rule_only_where_the_ping_pong_fold_runs():
 
 
 # fp32 grids the 1024-workgroup rule leaves under 256 work-groups take partitions down to 64 keys
-# until about 512 (measured: B1 H8 1K 0.050 -> 0.029 ms, B8 H3 N197 0.024 -> 0.015 ms); larger ones keep it
+# until about 512 (measured: B1 H8 1K 0.050 -> 0.029 ms, B8 H3 N197 0.024 -> 0.013 ms); larger ones keep it
 @pytest.mark.parametrize("n,bh,causal,parts,part", [
-    (1024, (1, 8), 0, 8, 128), (1024, (1, 8), 1, 8, 128), (197, (8, 3), 0, 3, 96), (512, (1, 8), 0, 8, 64),
+    (1024, (1, 8), 0, 8, 128), (1024, (1, 8), 1, 8, 128), (512, (1, 8), 0, 8, 64),
+    (197, (8, 3), 0, 4, 64),     # ceil(197 / 64) partitions: two stages per work-group, not three
+    (90, (1, 2), 0, 2, 64),
     (1025, (8, 3), 0, 2, 544),   # 432 work-groups already: two partitions (0.086 against 0.089 ms with three)
     (2048, (1, 8), 0, 4, 512), (4096, (1, 8), 0, 4, 1024),
 ])
