@@ -106,7 +106,11 @@ int plan_fwd(const elsa_fwd_args* a, elsa_fwd_plan* pl) {
     // short tail partition costs less than a third 32-key stage in every work-group: B8 H3 N197
     // 0.0154 -> 0.0127 ms (3 -> 4 partitions), B2 H3 N300 0.0149 -> 0.0131, B1 H2 N90 0.0124 ->
     // 0.0112 (1 -> 2)
-    if (a->dtype == ELSA_F32 && q_tiles * p < 256)
+    // Causal grids, whose work-groups above the diagonal return at once, fill below 512 work-groups
+    // too: B2 H8 N1024 causal 0.0515 -> 0.0380 ms (2 -> 4 partitions), B8 H3 N1025 causal 0.0656 ->
+    // 0.0644 (2 -> 3); non-causal ones there went both ways (B2 H8 N1024 0.051 -> 0.047, B8 H3 N1025
+    // 0.0856 -> 0.0890, B3 H8 N1024 0.083 -> 0.086) and keep the 256 bound.
+    if (a->dtype == ELSA_F32 && q_tiles * p < (a->is_causal ? 512 : 256))
       p = std::max<int64_t>(p, std::min<int64_t>(cdiv(512, q_tiles), cdiv(n, 64)));
     // fp16/bf16 grids at d <= 64 from 512 keys under 192 work-groups (a few heads of at most 2K rows):
     // partitions down to 128 keys until about 256 work-groups.  Forward ms (fp16 d64): B1 H8 1K 0.012

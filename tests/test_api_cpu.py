@@ -139,6 +139,8 @@ def test_plan_ping_pong_rule_only_where_the_ping_pong_fold_runs():
     (1024, (1, 8), 0, 8, 128), (1024, (1, 8), 1, 8, 128), (512, (1, 8), 0, 8, 64),
     (197, (8, 3), 0, 4, 64),     # ceil(197 / 64) partitions: two stages per work-group, not three
     (90, (1, 2), 0, 2, 64),
+    (1024, (2, 8), 1, 4, 256),   # causal: filled below 512 work-groups (half of them return at once)
+    (1024, (2, 8), 0, 2, 512),   # non-causal: 256 work-groups already
     (1025, (8, 3), 0, 2, 544),   # 432 work-groups already: two partitions (0.086 against 0.089 ms with three)
     (2048, (1, 8), 0, 4, 512), (4096, (1, 8), 0, 4, 1024),
 ])
